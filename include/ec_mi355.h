@@ -1,0 +1,182 @@
+/*
+ * ec_mi355.h — C ABI of the MI355X (gfx950) erasure-coding engine.
+ *
+ * The engine computes XOR parity and systematic Reed-Solomon codes over
+ * GF(2^8) (reduction polynomial x^8+x^4+x^3+x^2+1 = 0x11D, generator 0x02)
+ * on device-resident checkpoint shards, and reconstructs lost shards.
+ *
+ * Code conventions (fixed; every entry point follows them):
+ *   - generator matrix G = [ I_k ; C ] with the m x k Cauchy block
+ *       C[i][j] = inv((k + i) XOR j),   i in [0, m), j in [0, k);
+ *   - parity_i[b] = XOR_j C[i][j] * data_j[b] for every byte offset b;
+ *   - XOR parity is plain XOR of the data shards (not the m = 1 Cauchy row);
+ *   - matrices are row-major uint8 arrays in host memory.
+ *
+ * Where it plugs into the reference.  The reference (a Megatron-Core
+ * 0.14.0rc6 fork) has no erasure coder.  Its local ("non-persistent")
+ * checkpoint path hands the list of shard tensors of a
+ * MCoreTensorAwareStateDict to an external LocalCheckpointManager, whose
+ * redundancy step is a replication strategy injected at
+ *   megatron/training/training.py:825-835   (repl_strategy=...)
+ * and invoked from
+ *   megatron/training/checkpointing.py:538-541  (manager.save: encode here)
+ *   megatron/training/checkpointing.py:891-894  (manager.load: decode here)
+ * on the tensor list of
+ *   megatron/core/dist_checkpointing/tensor_aware_state_dict.py:179-243.
+ * Each entry point below names the slot of that path it serves.
+ *
+ * ABI conventions:
+ *   - every function returns EC_OK (0) or a negative EC_E* status; no C++
+ *     exception crosses this boundary;
+ *   - "d_" arguments are device pointers (HBM); other pointers are host;
+ *   - the caller owns every buffer; the library allocates no device memory;
+ *   - device work is enqueued on `stream` (a hipStream_t; NULL = the legacy
+ *     default stream) and is asynchronous with respect to the host;
+ *   - calls on different streams from different host threads are safe: the
+ *     library keeps no mutable global state.
+ */
+#ifndef EC_MI355_H
+#define EC_MI355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EC_ABI_VERSION 1
+
+/* Status codes. */
+#define EC_OK 0
+#define EC_EINVAL (-1)    /* bad argument: k, m, size, null pointer      */
+#define EC_EALIGN (-2)    /* pointer not 16-byte aligned where required   */
+#define EC_ESINGULAR (-3) /* matrix not invertible / too many erasures    */
+#define EC_EHIP (-4)      /* a HIP runtime call failed                    */
+#define EC_ERANGE (-5)    /* k, m or a length beyond the supported limits */
+
+/* Limits.  k + m <= 256 is what a Cauchy code over GF(2^8) allows; the
+ * device kernels take up to EC_MAX_K data and EC_MAX_M parity shards. */
+#define EC_MAX_K 32
+#define EC_MAX_M 16
+
+/* A hipStream_t, passed as an opaque pointer so that callers (ctypes, cgo,
+ * JNI) need no HIP header. */
+typedef void* ec_stream_t;
+
+/* ---- library identity and errors ------------------------------------ */
+
+/* Returns EC_ABI_VERSION of the built library. */
+int ec_abi_version(void);
+
+/* Human-readable text for a status code (static storage). */
+const char* ec_strerror(int status);
+
+/* ---- host-side GF(2^8) algebra (no device work) ---------------------- */
+
+/* Product of two field elements. */
+uint8_t ec_gf_mul(uint8_t a, uint8_t b);
+
+/* Multiplicative inverse; ec_gf_inv(0) returns 0. */
+uint8_t ec_gf_inv(uint8_t a);
+
+/* The m x k Cauchy parity block C[i][j] = inv((k+i) ^ j) into out[m*k].
+ * Replaces the fixed replica placement of the replication strategy built at
+ * megatron/training/training.py:825-828 with an m-of-(k+m) code. */
+int ec_cauchy_matrix(int k, int m, uint8_t* out);
+
+/* Gauss-Jordan inverse of the n x n matrix `in` into `out`.
+ * EC_ESINGULAR if it is not invertible. */
+int ec_gf_invert(const uint8_t* in, uint8_t* out, int n);
+
+/* Decode plan for the code [I_k ; coeff] (coeff is m x k) when the shard
+ * indices erased[0..n_erased) of the k+m shards are lost (data shards are
+ * 0..k-1, parity shards k..k+m-1).  Writes the k surviving shard indices
+ * used (ascending, the first k not erased) to survivors[k] and the
+ * n_erased x k matrix rows[] with lost_e = XOR_s rows[e][s] * survivor_s.
+ * Serves the load path at megatron/training/checkpointing.py:891-894.
+ * EC_ESINGULAR when n_erased > m. */
+int ec_decode_matrix(const uint8_t* coeff, int k, int m, const int* erased,
+                     int n_erased, int* survivors, uint8_t* rows);
+
+/* ---- device kernels --------------------------------------------------- */
+
+/* XOR parity: d_parity[b] = XOR_{j<k} d_data[j][b].  d_data is a host array
+ * of k device pointers.  Any alignment; 16-byte-aligned pointers take the
+ * vector path.  Serves manager.save at checkpointing.py:538-541 for m = 1. */
+int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity,
+                  uint64_t nbytes, ec_stream_t stream);
+
+/* Reed-Solomon encode: d_parity[i][b] = XOR_j coeff[i*k+j] * d_data[j][b].
+ * coeff is any m x k host matrix (normally ec_cauchy_matrix).  Serves
+ * manager.save at checkpointing.py:538-541. */
+int ec_rs_encode(const uint8_t* coeff, int k, int m,
+                 const uint8_t* const* d_data, uint8_t* const* d_parity,
+                 uint64_t nbytes, ec_stream_t stream);
+
+/* Reconstruct e lost shards from k survivors with the rows computed by
+ * ec_decode_matrix: d_out[r][b] = XOR_s rows[r*k+s] * d_survivors[s][b].
+ * Serves manager.load at checkpointing.py:891-894. */
+int ec_rs_decode(const uint8_t* rows, int k, int e,
+                 const uint8_t* const* d_survivors, uint8_t* const* d_out,
+                 uint64_t nbytes, ec_stream_t stream);
+
+/* Batched ragged encode: one launch over n_stripes stripes of k units of
+ * unit_bytes each.  Device arrays, row-major:
+ *   d_data_ptrs[s*k + j]   device address of unit j of stripe s (0 = absent)
+ *   d_data_len[s*k + j]    valid bytes of that unit (<= unit_bytes); the
+ *                          rest of the unit is taken as zeros
+ *   d_parity_ptrs[s*m + i] device address of parity unit i (unit_bytes)
+ * unit_bytes must be a multiple of 16 (EC_EALIGN otherwise) and at most
+ * 2 GiB (EC_ERANGE).  Units and
+ * parity units at 16-byte-aligned addresses take the vector path; others are
+ * read and written byte by byte, and no byte past a unit's valid length is
+ * read.  k <= 16 and m <= 4 (EC_ERANGE otherwise).  The units come from the ragged
+ * shard list of tensor_aware_state_dict.py:179-184 (MCoreTensorAwareStateDict
+ * .tensors), chunked in order. */
+int ec_encode_batched(const uint8_t* coeff, int k, int m,
+                      const uint64_t* d_data_ptrs, const uint32_t* d_data_len,
+                      const uint64_t* d_parity_ptrs, uint32_t n_stripes,
+                      uint32_t unit_bytes, ec_stream_t stream);
+
+/* Batched reconstruct: the stripes of an ec_encode_batched layout that lost
+ * the same e shard positions, recovered in one launch with the rows of
+ * ec_decode_matrix (e x k):
+ *   out_r = XOR_s rows[r*k+s] * survivor_s      for each stripe
+ *   d_surv_ptrs[s*k + t], d_surv_len[s*k + t]   the k surviving units of
+ *                                               stripe s (data or parity;
+ *                                               bytes past len read as zero)
+ *   d_out_ptrs[s*e + r], d_out_len[s*e + r]     where lost unit r goes and how
+ *                                               many of its bytes to write
+ *                                               (a data unit's valid length,
+ *                                               so a tensor's tail unit is
+ *                                               restored in place without
+ *                                               writing past its end)
+ * Same alignment rules and limits as ec_encode_batched (e <= 4).  Serves
+ * manager.load at checkpointing.py:891-894 for ragged shard lists. */
+int ec_decode_batched(const uint8_t* rows, int k, int e,
+                      const uint64_t* d_surv_ptrs, const uint32_t* d_surv_len,
+                      const uint64_t* d_out_ptrs, const uint32_t* d_out_len,
+                      uint32_t n_stripes, uint32_t unit_bytes,
+                      ec_stream_t stream);
+
+/* Incremental parity update over n_stripes changed stripes:
+ *   parity_i ^= XOR_j coeff[i*k+j] * (new_j ^ old_j)
+ * for every unit j whose d_new_ptrs[s*k+j] is non-zero (0 = unchanged unit,
+ * skipped).  d_old_ptrs holds the previous contents of the same units and
+ * d_len their valid bytes; d_parity_ptrs as in ec_encode_batched.  Stripes
+ * must be distinct (each parity unit is read-modified-written by one
+ * workgroup).  Same alignment rules and limits as ec_encode_batched.  Serves repeated
+ * manager.save calls (checkpointing.py:538-541) when only part of the state
+ * changed since the previous checkpoint. */
+int ec_parity_update(const uint8_t* coeff, int k, int m,
+                     const uint64_t* d_new_ptrs, const uint64_t* d_old_ptrs,
+                     const uint32_t* d_len, const uint64_t* d_parity_ptrs,
+                     uint32_t n_stripes, uint32_t unit_bytes,
+                     ec_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EC_MI355_H */

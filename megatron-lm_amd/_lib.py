@@ -1,0 +1,128 @@
+"""ctypes binding of the C ABI in ``include/ec_mi355.h`` (libec_mi355.so).
+
+The shared library is built in-tree by ``__graft_entry__.build()``.  There is
+no fallback: if the library is missing, every call raises
+``ECLibraryMissing``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_NAME = "libec_mi355.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+EC_OK = 0
+EC_EINVAL = -1
+EC_EALIGN = -2
+EC_ESINGULAR = -3
+EC_EHIP = -4
+EC_ERANGE = -5
+EC_MAX_K = 32
+EC_MAX_M = 16
+
+# Every symbol include/ec_mi355.h declares (tests check the export list).
+EXPORTS = (
+    "ec_abi_version",
+    "ec_strerror",
+    "ec_gf_mul",
+    "ec_gf_inv",
+    "ec_cauchy_matrix",
+    "ec_gf_invert",
+    "ec_decode_matrix",
+    "ec_xor_encode",
+    "ec_rs_encode",
+    "ec_rs_decode",
+    "ec_encode_batched",
+    "ec_decode_batched",
+    "ec_parity_update",
+)
+
+
+class ECLibraryMissing(RuntimeError):
+    pass
+
+
+class ECError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} (status {status})")
+
+
+class SingularError(ECError):
+    pass
+
+
+_lib = None
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ECLibraryMissing(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    L = ctypes.CDLL(LIB_PATH)
+    L.ec_abi_version.restype = _i
+    L.ec_abi_version.argtypes = []
+    if L.ec_abi_version() != ABI_VERSION:
+        raise ECLibraryMissing(f"{LIB_PATH} has ABI {L.ec_abi_version()}, expected {ABI_VERSION}")
+    L.ec_strerror.restype = ctypes.c_char_p
+    L.ec_strerror.argtypes = [_i]
+    L.ec_gf_mul.restype = ctypes.c_uint8
+    L.ec_gf_mul.argtypes = [ctypes.c_uint8, ctypes.c_uint8]
+    L.ec_gf_inv.restype = ctypes.c_uint8
+    L.ec_gf_inv.argtypes = [ctypes.c_uint8]
+    L.ec_cauchy_matrix.restype = _i
+    L.ec_cauchy_matrix.argtypes = [_i, _i, _u8p]
+    L.ec_gf_invert.restype = _i
+    L.ec_gf_invert.argtypes = [_u8p, _u8p, _i]
+    L.ec_decode_matrix.restype = _i
+    L.ec_decode_matrix.argtypes = [_u8p, _i, _i, ctypes.POINTER(_i), _i, ctypes.POINTER(_i), _u8p]
+    L.ec_xor_encode.restype = _i
+    L.ec_xor_encode.argtypes = [_vp, _i, _vp, _u64, _vp]
+    L.ec_rs_encode.restype = _i
+    L.ec_rs_encode.argtypes = [_u8p, _i, _i, _vp, _vp, _u64, _vp]
+    L.ec_rs_decode.restype = _i
+    L.ec_rs_decode.argtypes = [_u8p, _i, _i, _vp, _vp, _u64, _vp]
+    L.ec_encode_batched.restype = _i
+    L.ec_encode_batched.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _u32, _u32, _vp]
+    L.ec_decode_batched.restype = _i
+    L.ec_decode_batched.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
+    L.ec_parity_update.restype = _i
+    L.ec_parity_update.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
+    _lib = L
+    return L
+
+
+def strerror(status: int) -> str:
+    try:
+        return lib().ec_strerror(status).decode()
+    except ECLibraryMissing:
+        return "library not built"
+
+
+def check(status: int, what: str) -> None:
+    if status == EC_OK:
+        return
+    if status == EC_ESINGULAR:
+        raise SingularError(status, what)
+    raise ECError(status, what)
+
+
+def u8ptr(buf) -> "ctypes._Pointer":
+    """Pointer to a host uint8 numpy array."""
+    return buf.ctypes.data_as(_u8p)
+
+
+def ptr_array(addrs) -> ctypes.Array:
+    """Host array of device addresses (a `const uint8_t* const*`)."""
+    return (ctypes.c_void_p * len(addrs))(*[int(a) for a in addrs])

@@ -1,0 +1,152 @@
+"""Shard-level erasure coding of device tensors (flat shards of equal size).
+
+Every function takes contiguous HIP tensors (any dtype; their bytes are the
+shards, viewed without a copy) and enqueues the work on the given stream, or
+on torch's current stream, through the C ABI of ``include/ec_mi355.h``.
+
+The reference has no encoder; these are the operations its local-checkpoint
+redundancy slot (``repl_strategy`` built at megatron/training/training.py:825-835,
+used by ``manager.save`` at megatron/training/checkpointing.py:538-541 and
+``manager.load`` at :891-894) would call on one rank's shards.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+def _dev(t: torch.Tensor, what: str):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{what} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{what} must be a device (HIP) tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return t.data_ptr(), t.numel() * t.element_size()
+
+
+def stream_handle(stream: Optional[torch.cuda.Stream] = None) -> ctypes.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+# ------------------------------------------------------------ host algebra --
+
+def gf_mul(a: int, b: int) -> int:
+    return int(_lib.lib().ec_gf_mul(a, b))
+
+
+def gf_inv(a: int) -> int:
+    return int(_lib.lib().ec_gf_inv(a))
+
+
+def cauchy_matrix(k: int, m: int) -> np.ndarray:
+    """The m x k parity block C[i][j] = inv((k+i) ^ j) of G = [I_k ; C]."""
+    out = np.zeros((m, k), np.uint8)
+    _lib.check(_lib.lib().ec_cauchy_matrix(k, m, _lib.u8ptr(out)), "ec_cauchy_matrix")
+    return out
+
+
+def gf_invert(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.uint8)
+    n = a.shape[0]
+    if a.shape != (n, n):
+        raise ValueError("square matrix expected")
+    out = np.zeros((n, n), np.uint8)
+    _lib.check(_lib.lib().ec_gf_invert(_lib.u8ptr(a), _lib.u8ptr(out), n), "ec_gf_invert")
+    return out
+
+
+def decode_matrix(coeff: np.ndarray, erased: Sequence[int]):
+    """(survivors, rows): the k shard indices read and the e x k matrix that
+    maps them to the erased shards (data 0..k-1, parity k..k+m-1)."""
+    coeff = np.ascontiguousarray(coeff, np.uint8)
+    m, k = coeff.shape
+    e = len(erased)
+    er = (ctypes.c_int * max(1, e))(*erased)
+    surv = (ctypes.c_int * k)()
+    rows = np.zeros((max(1, e), k), np.uint8)
+    _lib.check(_lib.lib().ec_decode_matrix(_lib.u8ptr(coeff), k, m, er, e, surv,
+                                           _lib.u8ptr(rows)), "ec_decode_matrix")
+    return list(surv), rows[:e].copy()
+
+
+# ------------------------------------------------------------ device work --
+
+def _shards(shards: Sequence[torch.Tensor], what: str):
+    if len(shards) == 0:
+        raise ValueError(f"no {what}")
+    ptrs, sizes = zip(*[_dev(t, f"{what}[{i}]") for i, t in enumerate(shards)])
+    if len(set(sizes)) != 1:
+        raise ValueError(f"{what} differ in byte size: {sorted(set(sizes))}")
+    return list(ptrs), sizes[0]
+
+
+def _outputs(out, n: int, nbytes: int, device, what: str) -> List[torch.Tensor]:
+    if out is None:
+        return [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(n)]
+    out = list(out)
+    if len(out) != n:
+        raise ValueError(f"{what}: expected {n} tensors, got {len(out)}")
+    for i, t in enumerate(out):
+        _, nb = _dev(t, f"{what}[{i}]")
+        if nb != nbytes:
+            raise ValueError(f"{what}[{i}] has {nb} bytes, shards have {nbytes}")
+    return out
+
+
+def xor_encode(shards: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None,
+               stream=None) -> torch.Tensor:
+    """Single XOR parity of k equal-size shards."""
+    ptrs, nbytes = _shards(shards, "shards")
+    (out,) = _outputs(None if out is None else [out], 1, nbytes, shards[0].device, "out")
+    _lib.check(_lib.lib().ec_xor_encode(_lib.ptr_array(ptrs), len(ptrs), out.data_ptr(),
+                                        nbytes, stream_handle(stream)), "ec_xor_encode")
+    return out
+
+
+def matvec(coeff: np.ndarray, shards: Sequence[torch.Tensor], out=None, stream=None,
+           what: str = "ec_rs_encode") -> List[torch.Tensor]:
+    """out[i] = XOR_j coeff[i][j] * shards[j] (bytewise over GF(2^8))."""
+    coeff = np.ascontiguousarray(coeff, np.uint8)
+    m, k = coeff.shape
+    ptrs, nbytes = _shards(shards, "shards")
+    if len(ptrs) != k:
+        raise ValueError(f"coefficient matrix has {k} columns, got {len(ptrs)} shards")
+    outs = _outputs(out, m, nbytes, shards[0].device, "out")
+    fn = _lib.lib().ec_rs_encode if what == "ec_rs_encode" else _lib.lib().ec_rs_decode
+    _lib.check(fn(_lib.u8ptr(coeff), k, m, _lib.ptr_array(ptrs),
+                  _lib.ptr_array([t.data_ptr() for t in outs]), nbytes, stream_handle(stream)),
+               what)
+    return outs
+
+
+def rs_encode(shards: Sequence[torch.Tensor], m: int, coeff: Optional[np.ndarray] = None,
+              out=None, stream=None) -> List[torch.Tensor]:
+    """m Reed-Solomon parity shards of k equal-size data shards."""
+    k = len(shards)
+    coeff = cauchy_matrix(k, m) if coeff is None else coeff
+    return matvec(coeff, shards, out=out, stream=stream)
+
+
+def reconstruct(codeword: Sequence[Optional[torch.Tensor]], k: int, m: int,
+                coeff: Optional[np.ndarray] = None, out=None, stream=None) -> dict:
+    """Recover the missing (None) entries of a k+m codeword [data..., parity...].
+
+    Returns {shard index: recovered tensor}.  Raises SingularError when more
+    than m shards are missing."""
+    if len(codeword) != k + m:
+        raise ValueError(f"codeword must have k+m = {k + m} entries")
+    coeff = cauchy_matrix(k, m) if coeff is None else coeff
+    erased = [g for g, t in enumerate(codeword) if t is None]
+    if not erased:
+        return {}
+    surv, rows = decode_matrix(coeff, erased)
+    recovered = matvec(rows, [codeword[s] for s in surv], out=out, stream=stream,
+                       what="ec_rs_decode")
+    return dict(zip(erased, recovered))

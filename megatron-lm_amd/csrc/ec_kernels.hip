@@ -1,0 +1,646 @@
+// ec_kernels.hip — gfx950 kernels and the device entry points of the C ABI:
+// ec_xor_encode, ec_rs_encode, ec_rs_decode, ec_encode_batched,
+// ec_decode_batched, ec_parity_update.
+//
+// The work is byte-wise GF(2^8) arithmetic over HBM-resident shards: it is
+// bound by HBM bandwidth, not by the matrix cores, so everything here is
+// VALU code laid out for streaming.
+//
+// Data layout and mapping.
+//   A shard is a flat byte range.  Lane l of a 256-lane workgroup owns 16
+//   bytes (one global_load_dwordx4) of every shard at chunk index
+//   base + u*256 + l, u < U, so each wavefront reads 1 KiB contiguous per
+//   shard per load and the k loads of a lane are all in flight together.
+//   The m parity outputs of those bytes are accumulated in VGPRs and written
+//   once: every input byte is read from HBM exactly once and every parity
+//   byte written exactly once.
+//
+// GF multiply by a coefficient c (see PermTab in gf256.h): the byte x is cut
+// into fields x[2:0], x[5:3], x[7:6]; each field indexes an 8- or 4-entry
+// table of products held in one or two 32-bit registers, resolved for four
+// bytes at once by one v_perm_b32.  The three partial products and the
+// running parity are combined with v_bitop3_b32 (XOR3), so one coefficient
+// costs 3 permutes + 1.5 XOR3 per dword, and the field selectors (5 ops per
+// dword) are shared by all m outputs.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <array>
+#include <utility>
+
+#include "ec_mi355.h"
+#include "gf256.h"
+
+namespace ec {
+namespace {
+
+constexpr int kBlock = 256;     // lanes per workgroup (4 wavefronts)
+constexpr int kFastMaxK = 16;   // template-instantiated shard counts
+constexpr int kFastMaxM = 4;
+
+// ---------------------------------------------------------------- helpers --
+
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
+// Byte select from the 64-bit pair {hi:lo}: selector byte v in 0..7 returns
+// byte v of lo (v < 4) or byte v-4 of hi.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+struct Fields {
+  uint32_t f0, f1, f2;
+};
+
+__device__ __forceinline__ Fields fields(uint32_t w) {
+  return {w & 0x07070707u, (w >> 3) & 0x07070707u, (w >> 6) & 0x03030303u};
+}
+
+// acc ^= c*w for the four bytes of w (single coefficient).
+__device__ __forceinline__ uint32_t mac1(uint32_t acc, const PermTab& t, const Fields& f) {
+  acc = xor3(acc, perm(t.hi0, t.lo0, f.f0), perm(t.hi1, t.lo1, f.f1));
+  return acc ^ perm(t.t2, t.t2, f.f2);
+}
+
+// acc ^= a*wa ^ b*wb (two coefficients, six products, three XOR3).
+__device__ __forceinline__ uint32_t mac2(uint32_t acc, const PermTab& a, const Fields& fa,
+                                         const PermTab& b, const Fields& fb) {
+  acc = xor3(acc, perm(a.hi0, a.lo0, fa.f0), perm(a.hi1, a.lo1, fa.f1));
+  acc = xor3(acc, perm(a.t2, a.t2, fa.f2), perm(b.hi0, b.lo0, fb.f0));
+  return xor3(acc, perm(b.hi1, b.lo1, fb.f1), perm(b.t2, b.t2, fb.f2));
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int d) {
+  return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+}
+
+// Accumulate the products of all K shards for one 16-byte chunk:
+// acc[i][d] = XOR_j tab[i][j] * x[j].d
+template <int K, int M>
+__device__ __forceinline__ void gf_matvec16(uint32_t (&acc)[M][4], const uint4 (&x)[K],
+                                            const PermTab (&tab)[M][K]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int j = 0; j + 1 < K; j += 2) {
+      const Fields fa = fields(word(x[j], d));
+      const Fields fb = fields(word(x[j + 1], d));
+#pragma unroll
+      for (int i = 0; i < M; ++i) acc[i][d] = mac2(acc[i][d], tab[i][j], fa, tab[i][j + 1], fb);
+    }
+    if (K & 1) {
+      const Fields f = fields(word(x[K - 1], d));
+#pragma unroll
+      for (int i = 0; i < M; ++i) acc[i][d] = mac1(acc[i][d], tab[i][K - 1], f);
+    }
+  }
+}
+
+// Device-side field multiply (shift-and-reduce), used only to build the
+// permute tables of the generic kernel in LDS.
+__device__ uint8_t dev_gf_mul(uint32_t a, uint32_t b) {
+  uint32_t r = 0;
+  for (int i = 0; i < 8; ++i) {
+    if (b & 1u) r ^= a;
+    b >>= 1;
+    a <<= 1;
+    if (a & 0x100u) a ^= 0x11Du;
+  }
+  return (uint8_t)r;
+}
+
+__device__ PermTab dev_perm_tab(uint32_t c) {
+  PermTab p;
+  uint32_t w[5] = {0, 0, 0, 0, 0};
+  for (int a = 0; a < 8; ++a) {
+    w[a >> 2] |= (uint32_t)dev_gf_mul(c, a) << (8 * (a & 3));
+    w[2 + (a >> 2)] |= (uint32_t)dev_gf_mul(c, a << 3) << (8 * (a & 3));
+  }
+  for (int a = 0; a < 4; ++a) w[4] |= (uint32_t)dev_gf_mul(c, a << 6) << (8 * a);
+  p.lo0 = w[0];
+  p.hi0 = w[1];
+  p.lo1 = w[2];
+  p.hi1 = w[3];
+  p.t2 = w[4];
+  return p;
+}
+
+// ------------------------------------------------ fast matrix-vector kernel --
+// parity_i = XOR_j C[i][j] * data_j over n16 16-byte chunks; all pointers
+// 16-byte aligned.  Encode and decode both run this kernel (decode with the
+// host-inverted rows over the survivors).
+
+template <int K, int M>
+struct RsArgs {
+  const uint8_t* data[K];
+  uint8_t* out[M];
+  PermTab tab[M][K];
+  uint64_t n16;
+};
+
+template <int K, int M, int U>
+__global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
+  const uint64_t tile = (uint64_t)kBlock * U;
+  const uint64_t stride = (uint64_t)gridDim.x * tile;
+  for (uint64_t base = (uint64_t)blockIdx.x * tile + threadIdx.x; base < a.n16;
+       base += stride) {
+    uint4 x[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        x[u][j] = idx < a.n16 ? reinterpret_cast<const uint4*>(a.data[j])[idx]
+                              : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+      uint32_t acc[M][4] = {};
+      gf_matvec16<K, M>(acc, x[u], a.tab);
+      if (idx < a.n16) {
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+          reinterpret_cast<uint4*>(a.out[i])[idx] =
+              make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- XOR kernel --
+
+template <int K>
+struct XorArgs {
+  const uint8_t* data[K];
+  uint8_t* out;
+  uint64_t n16;
+};
+
+__device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uint4& c) {
+  return make_uint4(xor3(a.x, b.x, c.x), xor3(a.y, b.y, c.y), xor3(a.z, b.z, c.z),
+                    xor3(a.w, b.w, c.w));
+}
+
+template <int K, int U>
+__global__ void __launch_bounds__(kBlock) xor_kernel(const XorArgs<K> a) {
+  const uint64_t tile = (uint64_t)kBlock * U;
+  const uint64_t stride = (uint64_t)gridDim.x * tile;
+  for (uint64_t base = (uint64_t)blockIdx.x * tile + threadIdx.x; base < a.n16;
+       base += stride) {
+    uint4 x[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        x[u][j] = idx < a.n16 ? reinterpret_cast<const uint4*>(a.data[j])[idx]
+                              : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+      uint4 acc = x[u][0];
+      int j = 1;
+#pragma unroll
+      for (; j + 1 < K; j += 2) acc = xor3v(acc, x[u][j], x[u][j + 1]);
+      if (j < K)
+        acc = make_uint4(acc.x ^ x[u][j].x, acc.y ^ x[u][j].y, acc.z ^ x[u][j].z,
+                         acc.w ^ x[u][j].w);
+      if (idx < a.n16) reinterpret_cast<uint4*>(a.out)[idx] = acc;
+    }
+  }
+}
+
+// --------------------------------------------------------- generic kernel --
+// Any k <= EC_MAX_K, m <= EC_MAX_M and any alignment: byte loads and stores,
+// four bytes per lane, permute tables built in LDS by the workgroup.  Used for
+// shard counts beyond the instantiated ones, misaligned pointers and the
+// sub-16-byte tail of the fast kernels.
+
+struct GenArgs {
+  const uint8_t* data[EC_MAX_K];
+  uint8_t* out[EC_MAX_M];
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];
+  uint64_t n;
+  int k, m;
+};
+
+__global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
+  __shared__ PermTab tab[EC_MAX_M * EC_MAX_K];
+  for (int t = threadIdx.x; t < a.m * a.k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
+  __syncthreads();
+  const uint64_t n4 = (a.n + 3) / 4;
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t q = (uint64_t)blockIdx.x * kBlock + threadIdx.x; q < n4; q += stride) {
+    const uint64_t b0 = q * 4;
+    const int nb = (int)((a.n - b0) < 4 ? (a.n - b0) : 4);
+    uint32_t acc[EC_MAX_M];
+    for (int i = 0; i < a.m; ++i) acc[i] = 0;
+    for (int j = 0; j < a.k; ++j) {
+      uint32_t w = 0;
+      for (int b = 0; b < nb; ++b) w |= (uint32_t)a.data[j][b0 + b] << (8 * b);
+      const Fields f = fields(w);
+      for (int i = 0; i < a.m; ++i) acc[i] = mac1(acc[i], tab[i * a.k + j], f);
+    }
+    for (int i = 0; i < a.m; ++i)
+      for (int b = 0; b < nb; ++b) a.out[i][b0 + b] = (uint8_t)(acc[i] >> (8 * b));
+  }
+}
+
+// ------------------------------------------------ batched stripe kernels --
+// Grid = n_stripes x tiles_per_unit workgroups, stripe-major, so consecutive
+// workgroups stream adjacent bytes of the same k units.  The descriptor of a
+// stripe is uniform across the workgroup (scalar loads).
+
+// 16 bytes of a unit at byte offset off, zero beyond len.  A 16-byte-aligned
+// unit takes one dwordx4 load; the chunk that straddles len, and every chunk
+// of a misaligned unit, is read byte by byte, so nothing past len is read.
+__device__ __forceinline__ uint4 load_unit(const uint8_t* p, uint32_t off, uint32_t len) {
+  if (off + 16u <= len && (reinterpret_cast<uintptr_t>(p) & 15u) == 0)
+    return *reinterpret_cast<const uint4*>(p + off);
+  uint32_t w[4] = {0, 0, 0, 0};
+  for (uint32_t b = off; b < len && b < off + 16u; ++b)
+    w[(b - off) >> 2] |= (uint32_t)p[b] << (8 * ((b - off) & 3));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Store 16 parity bytes at byte offset off (byte stores if p is misaligned).
+__device__ __forceinline__ void store_unit(uint8_t* p, uint32_t off, const uint4& v) {
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+    *reinterpret_cast<uint4*>(p + off) = v;
+    return;
+  }
+  for (int b = 0; b < 16; ++b) p[off + b] = (uint8_t)(word(v, b >> 2) >> (8 * (b & 3)));
+}
+
+// Store the bytes of v that fall below len at byte offset off of p.
+__device__ __forceinline__ void store_unit_len(uint8_t* p, uint32_t off, uint32_t len,
+                                               const uint4& v) {
+  if (off + 16u <= len) {
+    store_unit(p, off, v);
+    return;
+  }
+  for (uint32_t b = off; b < len && b < off + 16u; ++b)
+    p[b] = (uint8_t)(word(v, (b - off) >> 2) >> (8 * ((b - off) & 3)));
+}
+
+template <int K, int M>
+struct BatchArgs {
+  const uint64_t* dptr;  // [n_stripes][K]
+  const uint32_t* dlen;  // [n_stripes][K]
+  const uint64_t* pptr;  // [n_stripes][M]
+  const uint32_t* olen;  // [n_stripes][M] valid output bytes, or null = whole units
+  PermTab tab[M][K];
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;
+};
+
+template <int K, int M, int U>
+__global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
+  const uint32_t s = blockIdx.x / a.tiles_per_unit;
+  const uint32_t t = blockIdx.x - s * a.tiles_per_unit;
+  const uint8_t* d[K];
+  uint32_t len[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
+    const uint32_t l = a.dlen[(uint64_t)s * K + j];
+    len[j] = d[j] ? (l < a.unit_bytes ? l : a.unit_bytes) : 0u;
+  }
+  const uint32_t base = t * (kBlock * U) + threadIdx.x;
+  uint4 x[U][K];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t off = (base + u * kBlock) * 16u;
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      x[u][j] = off < len[j] ? load_unit(d[j], off, len[j]) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t off = (base + u * kBlock) * 16u;
+    if (off >= a.unit_bytes) continue;
+    uint32_t acc[M][4] = {};
+    gf_matvec16<K, M>(acc, x[u], a.tab);
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+      const uint4 v = make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+      if (a.olen == nullptr) {
+        store_unit(p, off, v);
+      } else {
+        const uint32_t l = a.olen[(uint64_t)s * M + i];
+        if (p != nullptr && off < l) store_unit_len(p, off, l < a.unit_bytes ? l : a.unit_bytes, v);
+      }
+    }
+  }
+}
+
+template <int K, int M>
+struct UpdateArgs {
+  const uint64_t* nptr;  // [n_stripes][K], 0 = unit unchanged
+  const uint64_t* optr;  // [n_stripes][K]
+  const uint32_t* len;   // [n_stripes][K]
+  const uint64_t* pptr;  // [n_stripes][M]
+  PermTab tab[M][K];
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;
+};
+
+template <int K, int M>
+__global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a) {
+  const uint32_t s = blockIdx.x / a.tiles_per_unit;
+  const uint32_t t = blockIdx.x - s * a.tiles_per_unit;
+  const uint32_t off = (t * kBlock + threadIdx.x) * 16u;
+  if (off >= a.unit_bytes) return;
+  uint32_t acc[M][4] = {};
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const uint8_t* nw = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
+    if (nw == nullptr) continue;  // uniform: unchanged unit
+    const uint8_t* od = reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]);
+    uint32_t l = a.len[(uint64_t)s * K + j];
+    l = l < a.unit_bytes ? l : a.unit_bytes;
+    if (off >= l) continue;
+    const uint4 vn = load_unit(nw, off, l);
+    const uint4 vo = load_unit(od, off, l);
+    const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) {
+      const Fields f = fields(word(dl, dd));
+#pragma unroll
+      for (int i = 0; i < M; ++i) acc[i][dd] = mac1(acc[i][dd], a.tab[i][j], f);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    const uint4 v = load_unit(p, off, a.unit_bytes);
+    store_unit(p, off, make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]));
+  }
+}
+
+// ---------------------------------------------------------- host launch --
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int hip_status() { return hipGetLastError() == hipSuccess ? EC_OK : EC_EHIP; }
+
+// Grid for a grid-stride kernel over n16 chunks with U chunks per lane:
+// enough workgroups to cover the range once, capped so a launch stays a few
+// waves deep on 256 CUs.
+inline unsigned grid_for(uint64_t n16, int U) {
+  const uint64_t tiles = (n16 + (uint64_t)kBlock * U - 1) / ((uint64_t)kBlock * U);
+  const uint64_t cap = 1u << 20;
+  return (unsigned)(tiles < cap ? (tiles ? tiles : 1) : cap);
+}
+
+template <int K>
+constexpr int unroll_for() {
+  return K <= 8 ? 2 : 1;
+}
+
+template <int K, int M>
+int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, uint64_t n16,
+              hipStream_t st) {
+  RsArgs<K, M> a;
+  for (int j = 0; j < K; ++j) a.data[j] = d[j];
+  for (int i = 0; i < M; ++i) a.out[i] = o[i];
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  a.n16 = n16;
+  constexpr int U = unroll_for<K>();
+  hipLaunchKernelGGL((rs_kernel<K, M, U>), dim3(grid_for(n16, U)), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+template <int K>
+int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st) {
+  XorArgs<K> a;
+  for (int j = 0; j < K; ++j) a.data[j] = d[j];
+  a.out = o;
+  a.n16 = n16;
+  constexpr int U = unroll_for<K>();
+  hipLaunchKernelGGL((xor_kernel<K, U>), dim3(grid_for(n16, U)), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+template <int K, int M>
+int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
+                   const uint64_t* pptr, const uint32_t* olen, uint32_t n_stripes,
+                   uint32_t unit_bytes, hipStream_t st) {
+  BatchArgs<K, M> a;
+  a.dptr = dptr;
+  a.dlen = dlen;
+  a.pptr = pptr;
+  a.olen = olen;
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  constexpr int U = unroll_for<K>();
+  const uint32_t unit16 = unit_bytes / 16u;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
+  const uint64_t blocks = (uint64_t)n_stripes * a.tiles_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  hipLaunchKernelGGL((batched_kernel<K, M, U>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+template <int K, int M>
+int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* optr,
+                  const uint32_t* len, const uint64_t* pptr, uint32_t n_stripes,
+                  uint32_t unit_bytes, hipStream_t st) {
+  UpdateArgs<K, M> a;
+  a.nptr = nptr;
+  a.optr = optr;
+  a.len = len;
+  a.pptr = pptr;
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  const uint32_t unit16 = unit_bytes / 16u;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit16 + kBlock - 1) / kBlock;
+  const uint64_t blocks = (uint64_t)n_stripes * a.tiles_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  hipLaunchKernelGGL((update_kernel<K, M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+// Dispatch tables over the instantiated (K, M) grid.
+using RsFn = int (*)(const uint8_t*, const uint8_t* const*, uint8_t* const*, uint64_t,
+                     hipStream_t);
+using XorFn = int (*)(const uint8_t* const*, uint8_t*, uint64_t, hipStream_t);
+using BatchFn = int (*)(const uint8_t*, const uint64_t*, const uint32_t*, const uint64_t*,
+                        const uint32_t*, uint32_t, uint32_t, hipStream_t);
+using UpdFn = int (*)(const uint8_t*, const uint64_t*, const uint64_t*, const uint32_t*,
+                      const uint64_t*, uint32_t, uint32_t, hipStream_t);
+
+template <int K, int... Ms>
+constexpr auto rs_row(std::integer_sequence<int, Ms...>) {
+  return std::array<RsFn, sizeof...(Ms)>{&launch_rs<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto rs_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<RsFn, kFastMaxM>, sizeof...(Ks)>{
+      rs_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
+template <int K, int... Ms>
+constexpr auto batch_row(std::integer_sequence<int, Ms...>) {
+  return std::array<BatchFn, sizeof...(Ms)>{&launch_batched<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto batch_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<BatchFn, kFastMaxM>, sizeof...(Ks)>{
+      batch_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
+template <int K, int... Ms>
+constexpr auto upd_row(std::integer_sequence<int, Ms...>) {
+  return std::array<UpdFn, sizeof...(Ms)>{&launch_update<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto upd_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<UpdFn, kFastMaxM>, sizeof...(Ks)>{
+      upd_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
+template <int... Ks>
+constexpr auto xor_table(std::integer_sequence<int, Ks...>) {
+  return std::array<XorFn, sizeof...(Ks)>{&launch_xor<Ks + 1>...};
+}
+
+const auto kRsTable = rs_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kBatchTable = batch_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kUpdTable = upd_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kXorTable = xor_table(std::make_integer_sequence<int, kFastMaxK>{});
+
+int launch_generic(const uint8_t* coeff, int k, int m, const uint8_t* const* d,
+                   uint8_t* const* o, uint64_t offset, uint64_t n, hipStream_t st) {
+  GenArgs a;
+  for (int j = 0; j < k; ++j) a.data[j] = d[j] + offset;
+  for (int i = 0; i < m; ++i) a.out[i] = o[i] + offset;
+  for (int t = 0; t < m * k; ++t) a.coeff[t] = coeff[t];
+  a.n = n;
+  a.k = k;
+  a.m = m;
+  const uint64_t n4 = (n + 3) / 4;
+  uint64_t blocks = (n4 + kBlock - 1) / kBlock;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(generic_kernel, dim3((unsigned)(blocks ? blocks : 1)), dim3(kBlock), 0, st,
+                     a);
+  return hip_status();
+}
+
+int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t* const* o,
+           uint64_t nbytes, hipStream_t st) {
+  if (!coeff || !d || !o) return EC_EINVAL;
+  if (k < 1 || m < 1) return EC_EINVAL;
+  if (k > EC_MAX_K || m > EC_MAX_M) return EC_ERANGE;
+  bool aligned = true;
+  for (int j = 0; j < k; ++j) {
+    if (!d[j]) return EC_EINVAL;
+    aligned &= aligned16(d[j]);
+  }
+  for (int i = 0; i < m; ++i) {
+    if (!o[i]) return EC_EINVAL;
+    aligned &= aligned16(o[i]);
+  }
+  if (nbytes == 0) return EC_OK;
+  if (!aligned || k > kFastMaxK || m > kFastMaxM)
+    return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
+  const uint64_t n16 = nbytes / 16;
+  int s = EC_OK;
+  if (n16) s = kRsTable[k - 1][m - 1](coeff, d, o, n16, st);
+  if (s == EC_OK && (nbytes & 15))
+    s = launch_generic(coeff, k, m, d, o, n16 * 16, nbytes & 15, st);
+  return s;
+}
+
+int check_batch(const uint8_t* coeff, int k, int m, const void* a, const void* b,
+                const void* c, uint32_t unit_bytes) {
+  if (!coeff || !a || !b || !c || k < 1 || m < 1) return EC_EINVAL;
+  if (k > kFastMaxK || m > kFastMaxM) return EC_ERANGE;
+  if (unit_bytes == 0 || (unit_bytes & 15u)) return EC_EALIGN;
+  // Byte offsets inside a unit are 32-bit in the kernels, with one tile of
+  // headroom past the unit's end.
+  if (unit_bytes > (1u << 31)) return EC_ERANGE;
+  return EC_OK;
+}
+
+}  // namespace
+}  // namespace ec
+
+extern "C" {
+
+int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64_t nbytes,
+                  ec_stream_t stream) {
+  if (!d_data || !d_parity || k < 1) return EC_EINVAL;
+  if (k > EC_MAX_K) return EC_ERANGE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  bool aligned = ec::aligned16(d_parity);
+  for (int j = 0; j < k; ++j) {
+    if (!d_data[j]) return EC_EINVAL;
+    aligned &= ec::aligned16(d_data[j]);
+  }
+  if (nbytes == 0) return EC_OK;
+  uint8_t ones[EC_MAX_K];
+  for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
+  uint8_t* const out[1] = {d_parity};
+  if (!aligned || k > ec::kFastMaxK)
+    return ec::launch_generic(ones, k, 1, d_data, out, 0, nbytes, st);
+  const uint64_t n16 = nbytes / 16;
+  int s = EC_OK;
+  if (n16) s = ec::kXorTable[k - 1](d_data, d_parity, n16, st);
+  if (s == EC_OK && (nbytes & 15))
+    s = ec::launch_generic(ones, k, 1, d_data, out, n16 * 16, nbytes & 15, st);
+  return s;
+}
+
+int ec_rs_encode(const uint8_t* coeff, int k, int m, const uint8_t* const* d_data,
+                 uint8_t* const* d_parity, uint64_t nbytes, ec_stream_t stream) {
+  return ec::matvec(coeff, k, m, d_data, d_parity, nbytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_rs_decode(const uint8_t* rows, int k, int e, const uint8_t* const* d_survivors,
+                 uint8_t* const* d_out, uint64_t nbytes, ec_stream_t stream) {
+  return ec::matvec(rows, k, e, d_survivors, d_out, nbytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* d_data_ptrs,
+                      const uint32_t* d_data_len, const uint64_t* d_parity_ptrs,
+                      uint32_t n_stripes, uint32_t unit_bytes, ec_stream_t stream) {
+  int s = ec::check_batch(coeff, k, m, d_data_ptrs, d_data_len, d_parity_ptrs, unit_bytes);
+  if (s != EC_OK) return s;
+  if (n_stripes == 0) return EC_OK;
+  return ec::kBatchTable[k - 1][m - 1](coeff, d_data_ptrs, d_data_len, d_parity_ptrs, nullptr,
+                                       n_stripes, unit_bytes,
+                                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_decode_batched(const uint8_t* rows, int k, int e, const uint64_t* d_surv_ptrs,
+                      const uint32_t* d_surv_len, const uint64_t* d_out_ptrs,
+                      const uint32_t* d_out_len, uint32_t n_stripes, uint32_t unit_bytes,
+                      ec_stream_t stream) {
+  int s = ec::check_batch(rows, k, e, d_surv_ptrs, d_surv_len, d_out_ptrs, unit_bytes);
+  if (s != EC_OK) return s;
+  if (!d_out_len) return EC_EINVAL;
+  if (n_stripes == 0) return EC_OK;
+  return ec::kBatchTable[k - 1][e - 1](rows, d_surv_ptrs, d_surv_len, d_out_ptrs, d_out_len,
+                                       n_stripes, unit_bytes,
+                                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* d_new_ptrs,
+                     const uint64_t* d_old_ptrs, const uint32_t* d_len,
+                     const uint64_t* d_parity_ptrs, uint32_t n_stripes, uint32_t unit_bytes,
+                     ec_stream_t stream) {
+  int s = ec::check_batch(coeff, k, m, d_new_ptrs, d_old_ptrs, d_parity_ptrs, unit_bytes);
+  if (s != EC_OK) return s;
+  if (!d_len) return EC_EINVAL;
+  if (n_stripes == 0) return EC_OK;
+  return ec::kUpdTable[k - 1][m - 1](coeff, d_new_ptrs, d_old_ptrs, d_len, d_parity_ptrs,
+                                     n_stripes, unit_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

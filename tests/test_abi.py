@@ -1,0 +1,110 @@
+"""C ABI checks that need no GPU: libec_mi355.so loads, exports every symbol
+include/ec_mi355.h declares, its host-side algebra agrees with the oracle, and
+argument errors come back as status codes before any device work."""
+import ctypes
+import itertools
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import pyref
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ec_mi355.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ec_\w+)\s*\(", text)))
+
+
+def test_header_matches_binding(pkg):
+    assert declared_functions() == sorted(pkg._lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    so = pkg._lib.LIB_PATH
+    out = subprocess.run(["nm", "-D", "--defined-only", so], check=True, capture_output=True,
+                         text=True).stdout
+    exported = set(re.findall(r"\bT (ec_\w+)$", out, flags=re.M))
+    missing = set(declared_functions()) - exported
+    assert not missing, f"not exported: {sorted(missing)}"
+    L = pkg._lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name)
+
+
+def test_abi_version_and_strerror(pkg):
+    L = pkg._lib.lib()
+    assert L.ec_abi_version() == pkg._lib.ABI_VERSION
+    for st in (0, -1, -2, -3, -4, -5):
+        assert L.ec_strerror(st)
+    assert L.ec_strerror(-99) == b"unknown status"
+
+
+def test_host_gf_mul_inv_match_oracle(pkg):
+    t = pyref.mul_table()
+    L = pkg._lib.lib()
+    got = np.array([[L.ec_gf_mul(a, b) for b in range(256)] for a in range(256)], np.uint8)
+    assert np.array_equal(got, t)
+    assert [pkg.gf_inv(a) for a in range(256)] == [oracle.gf_inv(a) for a in range(256)]
+
+
+@pytest.mark.parametrize("k,m", [(4, 1), (6, 3), (8, 2), (12, 4), (16, 4), (32, 16), (200, 56)])
+def test_host_cauchy_matches_oracle(pkg, k, m):
+    assert np.array_equal(pkg.cauchy_matrix(k, m), oracle.cauchy(k, m))
+
+
+@pytest.mark.parametrize("k,m", [(6, 3), (12, 4), (8, 2)])
+def test_host_decode_matrix_all_patterns(pkg, k, m):
+    C = oracle.cauchy(k, m)
+    for e in range(1, m + 1):
+        for lost in itertools.combinations(range(k + m), e):
+            s1, r1 = pkg.decode_matrix(C, list(lost))
+            s2, r2 = oracle.decode_matrix(C, k, m, list(lost))
+            assert s1 == s2 and np.array_equal(r1, r2)
+
+
+def test_host_invert_and_errors(pkg):
+    rng = np.random.default_rng(1)
+    a = rng.integers(0, 256, (7, 7), dtype=np.uint8)
+    assert np.array_equal(pkg.gf_invert(a), oracle.gf_invert(a))
+    with pytest.raises(pkg.SingularError):
+        pkg.gf_invert(np.array([[3, 6], [1, 2]], np.uint8))
+    with pytest.raises(pkg.SingularError):
+        pkg.decode_matrix(pkg.cauchy_matrix(6, 3), [0, 1, 2, 3])
+    with pytest.raises(pkg.ECError):
+        pkg.decode_matrix(pkg.cauchy_matrix(6, 3), [0, 0])
+    with pytest.raises(pkg.ECError):
+        pkg.cauchy_matrix(200, 57)
+
+
+def test_device_entry_points_reject_bad_arguments(pkg):
+    """Validation happens on the host, before any HIP call (safe without a GPU)."""
+    L = pkg._lib.lib()
+    C = pkg.cauchy_matrix(6, 3)
+    c = C.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+    nulls = (ctypes.c_void_p * 6)()
+    assert L.ec_rs_encode(c, 6, 3, None, None, 16, None) == pkg._lib.EC_EINVAL
+    assert L.ec_rs_encode(c, 0, 3, nulls, nulls, 16, None) == pkg._lib.EC_EINVAL
+    assert L.ec_rs_encode(c, 33, 3, nulls, nulls, 16, None) == pkg._lib.EC_ERANGE
+    assert L.ec_rs_encode(c, 6, 3, nulls, nulls, 16, None) == pkg._lib.EC_EINVAL
+    assert L.ec_xor_encode(nulls, 4, None, 16, None) == pkg._lib.EC_EINVAL
+    assert L.ec_rs_decode(c, 6, 17, nulls, nulls, 16, None) == pkg._lib.EC_ERANGE
+    one = ctypes.c_void_p(16)
+    assert L.ec_encode_batched(c, 6, 3, one, one, one, 1, 100, None) == pkg._lib.EC_EALIGN
+    assert L.ec_encode_batched(c, 17, 3, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
+    assert L.ec_decode_batched(c, 6, 3, one, one, one, None, 1, 64, None) == pkg._lib.EC_EINVAL
+    assert L.ec_parity_update(c, 6, 3, one, one, None, one, 1, 64, None) == pkg._lib.EC_EINVAL
+
+
+def test_missing_library_fails_loudly(pkg, monkeypatch):
+    monkeypatch.setattr(pkg._lib, "_lib", None)
+    monkeypatch.setattr(pkg._lib, "LIB_PATH", "/nonexistent/libec_mi355.so")
+    with pytest.raises(pkg.ECLibraryMissing):
+        pkg.cauchy_matrix(6, 3)

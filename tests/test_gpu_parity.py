@@ -1,0 +1,263 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU
+oracle on the same seeded bytes.  Integer work, so the bar is byte equality.
+"""
+import itertools
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def _host(rng, k, n):
+    return [rng.integers(0, 256, n, dtype=np.uint8) for _ in range(k)]
+
+
+def _to_dev(arrays, dev, offset=0):
+    """Device copies; with offset > 0, views starting offset bytes into a
+    larger allocation (misaligned pointers)."""
+    out = []
+    for a in arrays:
+        buf = torch.empty(a.size + offset, dtype=torch.uint8, device=dev)
+        view = buf[offset:]
+        view.copy_(torch.from_numpy(a))
+        out.append(view)
+    return out
+
+
+def _eq(t, a):
+    torch.cuda.synchronize()
+    return np.array_equal(t.cpu().numpy(), a)
+
+
+def test_rs_encode_every_instantiated_shape(pkg, dev):
+    """All K in 1..16 x M in 1..4 (the template-instantiated fast kernels)."""
+    rng = np.random.default_rng(0)
+    n = 4096 * 3 + 16 * 5
+    for k in range(1, 17):
+        d = _host(rng, k, n)
+        dd = _to_dev(d, dev)
+        for m in range(1, 5):
+            C = oracle.cauchy(k, m)
+            par = pkg.rs_encode(dd, m)
+            want = oracle.rs_encode(C, d)
+            for i in range(m):
+                assert _eq(par[i], want[i]), f"k={k} m={m} parity {i}"
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 255, 4096, 65536 + 7, (1 << 20) + 5, 3 << 20])
+def test_rs_encode_sizes_and_tails(pkg, dev, n):
+    rng = np.random.default_rng(n)
+    d = _host(rng, 6, n)
+    par = pkg.rs_encode(_to_dev(d, dev), 3)
+    for p, w in zip(par, oracle.rs_encode(oracle.cauchy(6, 3), d)):
+        assert _eq(p, w)
+
+
+@pytest.mark.parametrize("offset", [1, 4, 8, 12])
+def test_rs_encode_misaligned(pkg, dev, offset):
+    rng = np.random.default_rng(offset)
+    n = 70001
+    d = _host(rng, 6, n)
+    dd = _to_dev(d, dev, offset)
+    out = _to_dev([np.zeros(n, np.uint8)] * 3, dev, offset)
+    pkg.rs_encode(dd, 3, out=out)
+    for p, w in zip(out, oracle.rs_encode(oracle.cauchy(6, 3), d)):
+        assert _eq(p, w)
+
+
+@pytest.mark.parametrize("k,m", [(20, 6), (32, 16), (17, 1), (5, 9)])
+def test_rs_encode_generic_kernel(pkg, dev, k, m):
+    rng = np.random.default_rng(k * m)
+    n = 12345
+    d = _host(rng, k, n)
+    par = pkg.rs_encode(_to_dev(d, dev), m)
+    for p, w in zip(par, oracle.rs_encode(oracle.cauchy(k, m), d)):
+        assert _eq(p, w)
+
+
+def test_rs_encode_arbitrary_coefficients(pkg, dev):
+    """Any m x k matrix, including zeros and ones (decode rows look like this)."""
+    rng = np.random.default_rng(7)
+    n = 50000
+    for k, m in [(6, 3), (12, 4), (3, 2)]:
+        C = rng.integers(0, 256, (m, k), dtype=np.uint8)
+        C[0, 0] = 0
+        C[-1, -1] = 1
+        d = _host(rng, k, n)
+        par = pkg.matvec(C, _to_dev(d, dev))
+        for p, w in zip(par, oracle.rs_encode(C, d)):
+            assert _eq(p, w)
+
+
+@pytest.mark.parametrize("k", list(range(1, 17)) + [20, 32])
+def test_xor_encode(pkg, dev, k):
+    rng = np.random.default_rng(100 + k)
+    for n, off in [(4096 * 5 + 48, 0), (777, 0), (9999, 3)]:
+        d = _host(rng, k, n)
+        p = pkg.xor_encode(_to_dev(d, dev, off))
+        assert _eq(p, oracle.xor_encode(d)), f"k={k} n={n} off={off}"
+
+
+@pytest.mark.parametrize("k,m", [(6, 3), (4, 1), (8, 2)])
+def test_decode_every_erasure_pattern(pkg, dev, k, m):
+    rng = np.random.default_rng(k * 10 + m)
+    n = 65536 + 16
+    d = _host(rng, k, n)
+    dd = _to_dev(d, dev)
+    cw = dd + pkg.rs_encode(dd, m)
+    for e in range(1, m + 1):
+        for lost in itertools.combinations(range(k + m), e):
+            rec = pkg.reconstruct([None if g in lost else t for g, t in enumerate(cw)], k, m)
+            torch.cuda.synchronize()
+            for g in lost:
+                assert torch.equal(rec[g], cw[g]), f"lost={lost} shard {g}"
+
+
+def test_decode_12_4_sampled_patterns(pkg, dev):
+    k, m = 12, 4
+    rng = np.random.default_rng(44)
+    dd = _to_dev(_host(rng, k, 200_000), dev)
+    cw = dd + pkg.rs_encode(dd, m)
+    pats = list(itertools.combinations(range(16), 4))
+    for idx in rng.choice(len(pats), 60, replace=False):
+        lost = pats[idx]
+        rec = pkg.reconstruct([None if g in lost else t for g, t in enumerate(cw)], k, m)
+        torch.cuda.synchronize()
+        assert all(torch.equal(rec[g], cw[g]) for g in lost), lost
+
+
+def test_too_many_erasures_rejected(pkg, dev):
+    dd = _to_dev(_host(np.random.default_rng(0), 6, 64), dev)
+    cw = dd + pkg.rs_encode(dd, 3)
+    with pytest.raises(pkg.SingularError):
+        pkg.reconstruct([None] * 4 + cw[4:], 6, 3)
+
+
+def test_side_stream(pkg, dev):
+    rng = np.random.default_rng(5)
+    d = _host(rng, 6, 1 << 20)
+    dd = _to_dev(d, dev)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        out = [torch.empty(1 << 20, dtype=torch.uint8, device=dev) for _ in range(3)]
+    pkg.rs_encode(dd, 3, out=out, stream=s)
+    s.synchronize()
+    for p, w in zip(out, oracle.rs_encode(oracle.cauchy(6, 3), d)):
+        assert np.array_equal(p.cpu().numpy(), w)
+
+
+# ------------------------------------------------------------------ golden --
+
+def test_golden_xor(pkg, dev):
+    g = np.load(os.path.join(GOLDEN, "xor_k4.npz"))
+    assert _eq(pkg.xor_encode(_to_dev(list(g["data"]), dev)), g["parity"])
+
+
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.startswith("rs_")))
+def test_golden_rs(pkg, dev, name):
+    g = np.load(os.path.join(GOLDEN, name))
+    k, m = int(g["k"]), int(g["m"])
+    dd = _to_dev(list(g["data"]), dev)
+    par = pkg.rs_encode(dd, m)
+    for i in range(m):
+        assert _eq(par[i], g["parity"][i])
+    er = [int(x) for x in g["erased"]]
+    cw = dd + par
+    rec = pkg.reconstruct([None if x in er else t for x, t in enumerate(cw)], k, m)
+    for r, e in enumerate(er):
+        assert _eq(rec[e], g["recovered"][r])
+
+
+# ---------------------------------------------------------------- batched --
+
+def _ragged_device(rng, dev, n_tensors, max_bytes, misalign=False):
+    """Device tensors of random byte sizes (some zero-length-free, some odd),
+    optionally as views at odd offsets of one arena."""
+    sizes = rng.integers(1, max_bytes, n_tensors)
+    host = [rng.integers(0, 256, s, dtype=np.uint8) for s in sizes]
+    if not misalign:
+        return host, [torch.from_numpy(h).to(dev) for h in host]
+    arena = torch.empty(int(sizes.sum()) + 7 * n_tensors, dtype=torch.uint8, device=dev)
+    views, off = [], 0
+    for h in host:
+        off += int(rng.integers(0, 7))
+        v = arena[off: off + h.size]
+        v.copy_(torch.from_numpy(h))
+        views.append(v)
+        off += h.size
+    return host, views
+
+
+def _oracle_layout_parity(layout, host, unit):
+    """Oracle parity of the same stripes, from host copies of the units."""
+    k, m = layout.k, layout.m
+    grid = []
+    for s in range(layout.n_stripes):
+        row = []
+        for j in range(k):
+            u = s * k + j
+            if u >= layout.n_units:
+                row.append(None)
+                continue
+            t, i = int(layout.unit_tensor[u]), int(layout.unit_index[u])
+            row.append(host[t][i * unit: (i + 1) * unit])
+        grid.append(row)
+    return oracle.encode_batched(layout.coeff, grid, layout.host_len, unit)
+
+
+@pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 4096, False), (8, 2, 1024, True),
+                                               (6, 3, 65536, False), (5, 1, 256, True)])
+def test_batched_encode_matches_oracle(pkg, dev, k, m, unit, misalign):
+    rng = np.random.default_rng(k * 7 + unit)
+    host, tensors = _ragged_device(rng, dev, 40, 6 * unit, misalign)
+    layout = pkg.StripeLayout(tensors, k, m, unit)
+    par = layout.encode()
+    torch.cuda.synchronize()
+    assert np.array_equal(par.cpu().numpy(), _oracle_layout_parity(layout, host, unit))
+
+
+@pytest.mark.parametrize("lost", [(0,), (3, 13), (0, 5, 12, 15), (12, 13, 14, 15), (1, 2, 3, 4)])
+def test_batched_decode_round_trip(pkg, dev, lost):
+    k, m, unit = 12, 4, 4096
+    rng = np.random.default_rng(sum(lost))
+    host, tensors = _ragged_device(rng, dev, 50, 5 * unit, misalign=True)
+    pset = pkg.encode(tensors, k, m, unit)
+    par_ref = pset.parity.clone()
+    # Erase: overwrite the lost positions of every stripe with junk.
+    for s in range(pset.layout.n_stripes):
+        for pos in lost:
+            u = s * k + pos
+            if pos < k and u < pset.layout.n_units:
+                pset.layout.unit_view(u).fill_(0xA5)
+            elif pos >= k:
+                pset.parity[s, pos - k].fill_(0x5A)
+    pkg.decode(pset, lost)
+    torch.cuda.synchronize()
+    for h, t in zip(host, tensors):
+        assert np.array_equal(t.cpu().numpy(), h)
+    assert torch.equal(pset.parity, par_ref)
+
+
+def test_batched_update_equals_reencode(pkg, dev):
+    k, m, unit = 12, 4, 2048
+    rng = np.random.default_rng(77)
+    host, tensors = _ragged_device(rng, dev, 60, 8 * unit)
+    pset = pkg.encode(tensors, k, m, unit)
+    lay = pset.layout
+    changed = np.sort(rng.choice(lay.n_units, max(1, lay.n_units // 10), replace=False))
+    olds = []
+    for u in changed:
+        v = lay.unit_view(int(u))
+        olds.append(v.clone())
+        v.copy_(torch.from_numpy(rng.integers(0, 256, v.numel(), dtype=np.uint8)))
+    pkg.update(pset, changed, olds)
+    fresh = lay.encode()
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity, fresh)
