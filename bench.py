@@ -97,6 +97,80 @@ def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host
     }
 
 
+def batched_configs(pkg, synth, dev, seed: int) -> dict:
+    """Configs 4 and 5 through the batched stripe launcher: data GB/s of one
+    launch (HIP events) and HBM traffic GB/s, with product-only checks (a
+    decode round trip; update == full re-encode)."""
+    import numpy as np
+    import torch
+    out = {}
+    # config 4: one rank's 20.8 GB buffer, RS(8,2), 4 MiB units (620 stripes)
+    buf = synth.gpt_rank_buffer(dev, seed)
+    lay = pkg.StripeLayout([buf], 8, 2, 4 * MiB)
+    par = lay.alloc_parity()
+    w, e = timed(lambda: lay.encode(par), 10, 2)
+    keep = (lay.unit_view(3).clone(), par[0, 1].clone())
+    lay.unit_view(3).zero_()
+    par[0, 1].zero_()
+    lay.decode(par, [3, 9], stripes=[0])
+    torch.cuda.synchronize()
+    if not (torch.equal(lay.unit_view(3), keep[0]) and torch.equal(par[0, 1], keep[1])):
+        raise AssertionError("RS(8,2) batched round trip failed")
+    out["rs82_20.8GB_GBps"] = round(lay.data_bytes / (w * 1e-3) / 1e9, 1)
+    out["rs82_20.8GB_traffic_GBps"] = round((lay.data_bytes + par.numel()) / (e * 1e-3) / 1e9, 1)
+    out["rs82_20.8GB_ms"] = round(e, 3)
+    log(f"config 4 RS(8,2) {lay.n_stripes} stripes: {out['rs82_20.8GB_GBps']} GB/s data")
+    del buf, lay, par, keep
+    torch.cuda.empty_cache()
+
+    # config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units, 1% update
+    sizes, kinds = synth.ragged_sizes(seed)
+    tensors = []
+    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
+        dt = torch.bfloat16 if kind == 0 else torch.float32
+        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
+        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
+        tensors.append(t)
+    lay = pkg.StripeLayout(tensors, 12, 4, 64 << 10)
+    par = lay.alloc_parity()
+    w, e = timed(lambda: lay.encode(par), 10, 2)
+    out["rs124_ragged_GBps"] = round(lay.data_bytes / (w * 1e-3) / 1e9, 1)
+    out["rs124_ragged_traffic_GBps"] = round((lay.data_bytes + par.numel()) / (e * 1e-3) / 1e9, 1)
+    out["rs124_ragged_data_GB"] = round(lay.data_bytes / 1e9, 2)
+    log(f"config 5 RS(12,4) {lay.n_units} units: {out['rs124_ragged_GBps']} GB/s data")
+    changed = synth.perturbed_units(seed, lay.n_units, 0.01)
+    olds = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    for u in changed.tolist():
+        v = lay.unit_view(u)
+        olds.append(v.clone())
+        v.copy_(torch.randint(0, 256, (v.numel(),), dtype=torch.uint8, device=dev, generator=g))
+    plan = lay.plan_update(par, changed, olds)
+    lay.run(plan)
+    fresh = lay.encode()
+    torch.cuda.synchronize()
+    if not torch.equal(par, fresh):
+        raise AssertionError("incremental update differs from a full re-encode")
+    del fresh
+    # each further run folds the same delta in again (timing only)
+    w, e = timed(lambda: lay.run(plan), 10, 2)
+    changed_bytes = int(lay.host_len.reshape(-1)[changed].sum())
+    upd_traffic = 2 * changed_bytes + 2 * plan.n_stripes * 4 * (64 << 10)
+    out["update_1pct_changed_GB"] = round(changed_bytes / 1e9, 3)
+    out["update_1pct_ms"] = round(e, 3)
+    out["update_1pct_traffic_GBps"] = round(upd_traffic / (e * 1e-3) / 1e9, 1)
+    lay.encode(par)  # repeated update runs toggled the parity; restore it
+    lost = [1, 7, 12, 14]
+    dplan = lay.plan_decode(par, lost)
+    w, e = timed(lambda: lay.run(dplan), 5, 1)
+    out["rs124_ragged_decode4_GBps"] = round(lay.data_bytes / (e * 1e-3) / 1e9, 1)
+    log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
+    del tensors, lay, par, olds, plan, dplan
+    torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(k: int, m: int, shard: int):
     """HBM bytes per RS(6,3) launch from the committed counter summary
     (profiles/rs_encode_6x256MiB_pmc.json: FETCH_SIZE and WRITE_SIZE per
@@ -145,6 +219,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batched", action="store_true",
+                    help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
     ap.add_argument("--mode", choices=["full", "headline", "pmc"], default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
@@ -217,6 +293,8 @@ def main() -> int:
     xor_gbs = 4 * 64 * MiB / (xwall * 1e-3) / 1e9
     log(f"XOR(4) {xor_gbs:.1f} GB/s data")
 
+    batched = {} if args.no_batched else batched_configs(pkg, synth, dev, args.seed)
+
     # ---- practical ceiling: device-to-device copy -------------------------
     src = torch.empty(k * shard, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
@@ -260,6 +338,7 @@ def main() -> int:
             "decode_GBps": round(dec_gbs, 2), "decode_lost": lost,
             "decode_kernel_us": round(dev_ms * 1e3, 2),
             "xor_4x64MiB_GBps": round(xor_gbs, 2), "xor_kernel_us": round(xev * 1e3, 2),
+            **batched,
             "d2d_copy_GBps": round(copy_gbs, 1),
             "encode_frac_of_copy": round(enc_traffic_gbs / copy_gbs, 4),
         },

@@ -18,7 +18,8 @@
 //   of the 8 XCDs walks its own contiguous slice of the shards.  Measured on
 //   MI355X for RS(6,3) over 256 MiB shards: plain loads/stores and tables in
 //   SGPRs 5.48 TB/s of HBM traffic; streaming access 5.90; plus LDS tables
-//   6.15; plus the XCD order 6.22.
+//   6.15; plus the XCD order 6.22 (see gf_matvec16 for the table-read order
+//   that keeps wider codes at the same rate).
 //
 // GF multiply by a coefficient c (see PermTab in gf256.h): the byte x is cut
 // into fields x[2:0], x[5:3], x[7:6]; each field indexes an 8- or 4-entry
@@ -83,16 +84,25 @@ __device__ __forceinline__ uint32_t word(const uint4& v, int d) {
 
 // Streaming (non-temporal) 16-byte global accesses: every shard byte is
 // touched once, so nothing is worth keeping in L2 or the Infinity Cache.
+// Addresses are cast to the global address space: pointers read from
+// descriptor arrays are otherwise generic and compile to flat loads.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+typedef __attribute__((address_space(1))) uint8_t global_u8;
+
+__device__ __forceinline__ const global_u8* gptr(const void* p) {
+  return (const global_u8*)(uintptr_t)p;
+}
+__device__ __forceinline__ global_u8* gptr(void* p) { return (global_u8*)(uintptr_t)p; }
 
 __device__ __forceinline__ uint4 load_stream(const void* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 v = __builtin_nontemporal_load((const global_u32x4*)(uintptr_t)p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
   const u32x4 w = {v.x, v.y, v.z, v.w};
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+  __builtin_nontemporal_store(w, (global_u32x4*)(uintptr_t)p);
 }
 
 // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
@@ -118,22 +128,72 @@ __device__ __forceinline__ void stage_tables(PermTab (&dst)[M][K], const PermTab
 
 // Accumulate the products of all K shards for one 16-byte chunk:
 // acc[i][d] = XOR_j tab[i][j] * x[j].d
+//
+// Two loop orders, picked at compile time by the table footprint 5*M*K:
+//  - small codes (M*K <= 20, e.g. RS(6,3), RS(8,2)): d -> j -> i, and the
+//    compiler keeps every table in VGPRs for the whole kernel (<= 100
+//    registers), so no LDS traffic at all in the loop;
+//  - wider codes: j (in pairs) -> i -> d, the selectors of x[j], x[j+1] are
+//    computed once for all outputs and each coefficient's table is read from
+//    LDS once per chunk, right before its four uses.  The empty asm with a
+//    memory clobber stops the compiler from hoisting those reads out of the
+//    grid-stride loop: kept live in VGPRs, the tables alone would need 240
+//    registers for RS(12,4) (one wave per SIMD, no latency hiding).
+// Measured on MI355X (HBM traffic): RS(12,4) 3.2 TB/s with hoisted tables vs
+// 5.9 with per-use reads; RS(16,4) 0.8 vs 5.3; RS(6,3) 6.0-6.2 hoisted vs
+// 5.6 per-use.
+template <int K, int M>
+constexpr bool tables_in_registers() {
+  return K * M <= 20;
+}
+
 template <int K, int M>
 __device__ __forceinline__ void gf_matvec16(uint32_t (&acc)[M][4], const uint4 (&x)[K],
                                             const PermTab (&tab)[M][K]) {
+  if constexpr (tables_in_registers<K, M>()) {
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int j = 0; j + 1 < K; j += 2) {
+        const Fields fa = fields(word(x[j], d));
+        const Fields fb = fields(word(x[j + 1], d));
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[i][d] = mac2(acc[i][d], tab[i][j], fa, tab[i][j + 1], fb);
+      }
+      if (K & 1) {
+        const Fields f = fields(word(x[K - 1], d));
+#pragma unroll
+        for (int i = 0; i < M; ++i) acc[i][d] = mac1(acc[i][d], tab[i][K - 1], f);
+      }
+    }
+  } else {
 #pragma unroll
     for (int j = 0; j + 1 < K; j += 2) {
-      const Fields fa = fields(word(x[j], d));
-      const Fields fb = fields(word(x[j + 1], d));
+      Fields fa[4], fb[4];
 #pragma unroll
-      for (int i = 0; i < M; ++i) acc[i][d] = mac2(acc[i][d], tab[i][j], fa, tab[i][j + 1], fb);
+      for (int d = 0; d < 4; ++d) {
+        fa[d] = fields(word(x[j], d));
+        fb[d] = fields(word(x[j + 1], d));
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        asm volatile("" ::: "memory");
+        const PermTab ta = tab[i][j], tb = tab[i][j + 1];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[i][d] = mac2(acc[i][d], ta, fa[d], tb, fb[d]);
+      }
     }
     if (K & 1) {
-      const Fields f = fields(word(x[K - 1], d));
+      Fields f[4];
 #pragma unroll
-      for (int i = 0; i < M; ++i) acc[i][d] = mac1(acc[i][d], tab[i][K - 1], f);
+      for (int d = 0; d < 4; ++d) f[d] = fields(word(x[K - 1], d));
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        asm volatile("" ::: "memory");
+        const PermTab t = tab[i][K - 1];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[i][d] = mac1(acc[i][d], t, f[d]);
+      }
     }
   }
 }
@@ -192,9 +252,13 @@ __global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint64_t idx = base + (uint64_t)u * kBlock;
+      if (idx < a.n16) {
 #pragma unroll
-      for (int j = 0; j < K; ++j)
-        x[u][j] = idx < a.n16 ? load_stream(a.data[j] + idx * 16) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
+      } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -234,9 +298,13 @@ __global__ void __launch_bounds__(kBlock) xor_kernel(const XorArgs<K> a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint64_t idx = base + (uint64_t)u * kBlock;
+      if (idx < a.n16) {
 #pragma unroll
-      for (int j = 0; j < K; ++j)
-        x[u][j] = idx < a.n16 ? load_stream(a.data[j] + idx * 16) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
+      } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -300,9 +368,11 @@ __global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
 __device__ __forceinline__ uint4 load_unit(const uint8_t* p, uint32_t off, uint32_t len) {
   if (off + 16u <= len && (reinterpret_cast<uintptr_t>(p) & 15u) == 0)
     return load_stream(p + off);
+  const global_u8* g = gptr(p);
   uint32_t w[4] = {0, 0, 0, 0};
-  for (uint32_t b = off; b < len && b < off + 16u; ++b)
-    w[(b - off) >> 2] |= (uint32_t)p[b] << (8 * ((b - off) & 3));
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    if (off + b < len) w[b >> 2] |= (uint32_t)g[off + b] << (8 * (b & 3));
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -312,7 +382,9 @@ __device__ __forceinline__ void store_unit(uint8_t* p, uint32_t off, const uint4
     store_stream(p + off, v);
     return;
   }
-  for (int b = 0; b < 16; ++b) p[off + b] = (uint8_t)(word(v, b >> 2) >> (8 * (b & 3)));
+  global_u8* g = gptr(p);
+#pragma unroll
+  for (int b = 0; b < 16; ++b) g[off + b] = (uint8_t)(word(v, b >> 2) >> (8 * (b & 3)));
 }
 
 // Store the bytes of v that fall below len at byte offset off of p.
@@ -322,8 +394,10 @@ __device__ __forceinline__ void store_unit_len(uint8_t* p, uint32_t off, uint32_
     store_unit(p, off, v);
     return;
   }
-  for (uint32_t b = off; b < len && b < off + 16u; ++b)
-    p[b] = (uint8_t)(word(v, (b - off) >> 2) >> (8 * ((b - off) & 3)));
+  global_u8* g = gptr(p);
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    if (off + b < len) g[off + b] = (uint8_t)(word(v, b >> 2) >> (8 * (b & 3)));
 }
 
 template <int K, int M>
@@ -334,49 +408,109 @@ struct BatchArgs {
   const uint32_t* olen;  // [n_stripes][M] valid output bytes, or null = whole units
   PermTab tab[M][K];
   uint32_t unit_bytes;
-  uint32_t tiles_per_unit;
+  uint32_t tiles_per_unit;   // tiles of kBlock*U*16 bytes in a unit
+  uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
+  uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
 };
 
+// One tile of a stripe whose k units and m outputs all extend past the tile
+// and are 16-byte aligned (almost every tile): the flat kernel's inner loop.
 template <int K, int M, int U>
-__global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
-  __shared__ PermTab tab[M][K];
-  stage_tables<K, M>(tab, a.tab);
-  const uint32_t s = blockIdx.x / a.tiles_per_unit;
-  const uint32_t t = blockIdx.x - s * a.tiles_per_unit;
-  const uint8_t* d[K];
-  uint32_t len[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
-    const uint32_t l = a.dlen[(uint64_t)s * K + j];
-    len[j] = d[j] ? (l < a.unit_bytes ? l : a.unit_bytes) : 0u;
-  }
-  const uint32_t base = t * (kBlock * U) + threadIdx.x;
+__device__ __forceinline__ void tile_full(const uint8_t* const (&d)[K], uint8_t* const (&p)[M],
+                                          uint32_t base, const PermTab (&tab)[M][K]) {
   uint4 x[U][K];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint32_t off = (base + u * kBlock) * 16u;
 #pragma unroll
-    for (int j = 0; j < K; ++j)
-      x[u][j] = off < len[j] ? load_unit(d[j], off, len[j]) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < K; ++j) x[u][j] = load_stream(d[j] + off);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint32_t off = (base + u * kBlock) * 16u;
-    if (off >= a.unit_bytes) continue;
     uint32_t acc[M][4] = {};
     gf_matvec16<K, M>(acc, x[u], tab);
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-      uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
-      const uint4 v = make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-      if (a.olen == nullptr) {
-        store_unit(p, off, v);
-      } else {
-        const uint32_t l = a.olen[(uint64_t)s * M + i];
-        if (p != nullptr && off < l) store_unit_len(p, off, l < a.unit_bytes ? l : a.unit_bytes, v);
+    for (int i = 0; i < M; ++i)
+      store_stream(p[i] + off, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+  }
+}
+
+// Any other tile (a unit or output ending inside it, an absent unit, a
+// misaligned address): one unit at a time, descriptors re-read from memory,
+// byte-granular at the ends.  Kept as a rolled loop so that its registers
+// stay below the fast path's (the allocator takes the larger of the two).
+template <int K, int M, int U>
+__device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, uint32_t base,
+                                          const PermTab (&tab)[M][K]) {
+  for (int u = 0; u < U; ++u) {
+    const uint32_t off = (base + u * kBlock) * 16u;
+    if (off >= a.unit_bytes) continue;
+    uint32_t acc[M][4] = {};
+#pragma unroll 1
+    for (int j = 0; j < K; ++j) {
+      const uint8_t* dj = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
+      uint32_t lj = dj ? a.dlen[(uint64_t)s * K + j] : 0u;
+      lj = lj < a.unit_bytes ? lj : a.unit_bytes;
+      if (off >= lj) continue;
+      const uint4 xj = load_unit(dj, off, lj);
+      Fields f[4];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(xj, dd));
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        const PermTab t = tab[i][j];
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
       }
     }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      uint8_t* pi = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+      uint32_t li = a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes;
+      li = pi ? (li < a.unit_bytes ? li : a.unit_bytes) : 0u;
+      if (off < li)
+        store_unit_len(pi, off, li, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  }
+}
+
+template <int K, int M, int U>
+__global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  // Workgroup b covers tiles [t0, t1) of one stripe: the descriptor loads and
+  // table staging are paid once per span, not once per 4-8 KiB tile.
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  // Stripe-uniform facts (scalar registers): addresses, the shortest input
+  // and output extent, and whether everything is 16-byte aligned.
+  const uint8_t* d[K];
+  uint32_t full = a.unit_bytes;
+  bool aligned = true;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
+    const uint32_t l = d[j] ? a.dlen[(uint64_t)s * K + j] : 0u;
+    full = l < full ? l : full;
+    aligned &= (reinterpret_cast<uintptr_t>(d[j]) & 15u) == 0;
+  }
+  uint8_t* p[M];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    const uint32_t l = p[i] ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
+    full = l < full ? l : full;
+    aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+  }
+  constexpr uint32_t kTileBytes = kBlock * U * 16u;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t base = t * (kBlock * U) + threadIdx.x;
+    if (aligned && (t + 1) * kTileBytes <= full)
+      tile_full<K, M, U>(d, p, base, tab);
+    else
+      tile_edge<K, M, U>(a, s, base, tab);
   }
 }
 
@@ -411,11 +545,15 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     const uint4 vn = load_unit(nw, off, l);
     const uint4 vo = load_unit(od, off, l);
     const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
+    Fields f[4];
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) {
-      const Fields f = fields(word(dl, dd));
+    for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(dl, dd));
 #pragma unroll
-      for (int i = 0; i < M; ++i) acc[i][dd] = mac1(acc[i][dd], tab[i][j], f);
+    for (int i = 0; i < M; ++i) {
+      asm volatile("" ::: "memory");
+      const PermTab tj = tab[i][j];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], tj, f[dd]);
     }
   }
 #pragma unroll
@@ -486,7 +624,17 @@ int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* d
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
   a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
-  const uint64_t blocks = (uint64_t)n_stripes * a.tiles_per_unit;
+  // A workgroup walks up to 64 KiB of each unit, keeping at least 2048
+  // workgroups (8 per CU) in the launch.
+  const uint32_t tile_bytes = kBlock * U * 16u;
+  uint64_t tpb = (64u << 10) / tile_bytes;
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
   hipLaunchKernelGGL((batched_kernel<K, M, U>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
   return hip_status();

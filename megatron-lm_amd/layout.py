@@ -13,13 +13,49 @@ live.  One batched launch then encodes, decodes or updates every stripe.
 """
 from __future__ import annotations
 
-from typing import Dict, List, Optional, Sequence
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
 
 import numpy as np
 import torch
 
 from . import _lib
 from .codec import _dev, cauchy_matrix, decode_matrix, stream_handle
+
+
+def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
+    """Cut tensors (device base addresses ``base``, byte sizes ``size``), in
+    order, into units of ``unit_bytes`` and group them into stripes of k.
+
+    Returns (unit_tensor, unit_index, ptrs, lens): for each unit its tensor
+    and its index inside that tensor, and [n_stripes, k] arrays of unit
+    addresses (0 = absent slot of the last stripe) and valid lengths.
+    Zero-byte tensors contribute no unit; an empty list gives one empty
+    stripe."""
+    base = np.asarray(base, np.uint64)
+    size = np.asarray(size, np.int64)
+    n_units = (size + unit_bytes - 1) // unit_bytes
+    unit_tensor = np.repeat(np.arange(size.size), n_units)
+    first = np.concatenate([[0], np.cumsum(n_units)[:-1]]).astype(np.int64)
+    unit_index = np.arange(unit_tensor.size) - np.repeat(first, n_units)
+    total = int(unit_tensor.size)
+    n_stripes = max(1, (total + k - 1) // k)
+    ptr = np.zeros(n_stripes * k, np.uint64)
+    ln = np.zeros(n_stripes * k, np.uint32)
+    off = unit_index.astype(np.uint64) * np.uint64(unit_bytes)
+    ptr[:total] = base[unit_tensor] + off
+    ln[:total] = np.minimum(size[unit_tensor] - off.astype(np.int64), unit_bytes).astype(np.uint32)
+    return unit_tensor, unit_index, ptr.reshape(n_stripes, k), ln.reshape(n_stripes, k)
+
+
+@dataclass
+class BatchPlan:
+    """Device descriptors of one batched decode or update launch."""
+    kind: str                 # "decode" or "update"
+    rows: np.ndarray          # e x k decode rows, or the m x k coefficients
+    outputs: int              # rows of output per stripe (e, or m)
+    n_stripes: int
+    desc: Tuple[torch.Tensor, ...]
 
 
 def _hold(stream, *tensors) -> None:
@@ -56,22 +92,10 @@ class StripeLayout:
             p, nb = _dev(t, f"tensors[{i}]")
             base[i], size[i] = p, nb
         self.tensor_bytes = size
-        n_units = (size + unit_bytes - 1) // unit_bytes
-        self.unit_tensor = np.repeat(np.arange(len(size)), n_units)       # owning tensor
-        first = np.concatenate([[0], np.cumsum(n_units)[:-1]]).astype(np.int64)
-        self.unit_index = np.arange(self.unit_tensor.size) - np.repeat(first, n_units)
-        self.unit_first = first                                          # first unit per tensor
+        (self.unit_tensor, self.unit_index, self.host_ptrs,
+         self.host_len) = unit_table(base, size, k, unit_bytes)
         self.n_units = int(self.unit_tensor.size)
-        self.n_stripes = max(1, (self.n_units + k - 1) // k)
-        slots = self.n_stripes * k
-        ptr = np.zeros(slots, np.uint64)
-        ln = np.zeros(slots, np.uint32)
-        off = self.unit_index.astype(np.uint64) * np.uint64(unit_bytes)
-        ptr[: self.n_units] = base[self.unit_tensor] + off
-        ln[: self.n_units] = np.minimum(size[self.unit_tensor] - off.astype(np.int64),
-                                        unit_bytes).astype(np.uint32)
-        self.host_ptrs = ptr.reshape(self.n_stripes, k)
-        self.host_len = ln.reshape(self.n_stripes, k)
+        self.n_stripes = self.host_ptrs.shape[0]
         self.data_bytes = int(size.sum())
         self.d_ptrs = torch.from_numpy(self.host_ptrs.view(np.int64).copy()).to(self.device)
         self.d_len = torch.from_numpy(self.host_len.view(np.int32).copy()).to(self.device)
@@ -83,9 +107,7 @@ class StripeLayout:
                            device=self.device)
 
     def _parity_ptrs(self, parity: torch.Tensor) -> torch.Tensor:
-        if parity.shape != (self.n_stripes, self.m, self.unit_bytes) or parity.dtype != torch.uint8:
-            raise ValueError("parity must be uint8 [n_stripes, m, unit_bytes]")
-        _dev(parity, "parity")
+        self._parity_ptrs_check(parity)
         base = parity.data_ptr()
         idx = np.arange(self.n_stripes * self.m, dtype=np.uint64) * np.uint64(self.unit_bytes)
         return torch.from_numpy((idx + np.uint64(base)).view(np.int64)).to(self.device)
@@ -93,7 +115,13 @@ class StripeLayout:
     def encode(self, parity: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
         """All parity units in one launch: parity[s, i] = XOR_j C[i][j] * unit[s, j]."""
         parity = self.alloc_parity() if parity is None else parity
-        pp = self._parity_ptrs(parity)
+        cached = getattr(self, "_pp", None)
+        if cached is None or cached[0] != parity.data_ptr():
+            cached = (parity.data_ptr(), self._parity_ptrs(parity))
+            self._pp = cached
+        else:
+            self._parity_ptrs_check(parity)
+        pp = cached[1]
         _lib.check(_lib.lib().ec_encode_batched(
             _lib.u8ptr(self.coeff), self.k, self.m, self.d_ptrs.data_ptr(), self.d_len.data_ptr(),
             pp.data_ptr(), self.n_stripes, self.unit_bytes, stream_handle(stream)),
@@ -101,22 +129,30 @@ class StripeLayout:
         _hold(stream, pp)
         return parity
 
+    def _parity_ptrs_check(self, parity: torch.Tensor) -> None:
+        if parity.shape != (self.n_stripes, self.m, self.unit_bytes) or parity.dtype != torch.uint8:
+            raise ValueError("parity must be uint8 [n_stripes, m, unit_bytes]")
+        _dev(parity, "parity")
+
+    def _to_dev(self, a: np.ndarray, dt) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(a).view(dt).copy()).to(self.device)
+
     # ------------------------------------------------------------ decode --
 
-    def decode(self, parity: torch.Tensor, lost: Sequence[int],
-               stripes: Optional[np.ndarray] = None, stream=None) -> None:
-        """Rebuild, in place, the units at codeword positions ``lost`` (data
-        positions 0..k-1 into the tensors, parity positions k..k+m-1 into
-        ``parity``) of the given stripes (default: all).  The lost units'
-        current bytes are ignored; at most m positions."""
+    def plan_decode(self, parity: torch.Tensor, lost: Sequence[int],
+                    stripes: Optional[np.ndarray] = None) -> Optional[BatchPlan]:
+        """Descriptors for rebuilding the units at codeword positions ``lost``
+        (data positions 0..k-1 into the tensors, parity positions k..k+m-1
+        into ``parity``) of the given stripes (default: all); at most m
+        positions.  None if nothing is lost."""
         lost = sorted(set(int(x) for x in lost))
         if not lost:
-            return
+            return None
         k, m = self.k, self.m
         surv, rows = decode_matrix(self.coeff, lost)
         st = np.arange(self.n_stripes) if stripes is None else np.asarray(stripes, np.int64)
+        self._parity_ptrs_check(parity)
         par_base = np.uint64(parity.data_ptr())
-        self._parity_ptrs(parity)
 
         def slot(pos):
             if pos < k:
@@ -133,27 +169,32 @@ class StripeLayout:
         ol = np.zeros((st.size, len(lost)), np.uint32)
         for r, pos in enumerate(lost):
             op[:, r], ol[:, r] = slot(pos)
-        dev = lambda a, dt: torch.from_numpy(a.view(dt).copy()).to(self.device)
-        d_sp, d_sl, d_op, d_ol = dev(sp, np.int64), dev(sl, np.int32), dev(op, np.int64), dev(ol, np.int32)
-        _lib.check(_lib.lib().ec_decode_batched(
-            _lib.u8ptr(rows), k, len(lost), d_sp.data_ptr(), d_sl.data_ptr(), d_op.data_ptr(),
-            d_ol.data_ptr(), int(st.size), self.unit_bytes, stream_handle(stream)),
-            "ec_decode_batched")
-        _hold(stream, d_sp, d_sl, d_op, d_ol)
+        return BatchPlan("decode", rows, len(lost), int(st.size),
+                         (self._to_dev(sp, np.int64), self._to_dev(sl, np.int32),
+                          self._to_dev(op, np.int64), self._to_dev(ol, np.int32)))
+
+    def decode(self, parity: torch.Tensor, lost: Sequence[int],
+               stripes: Optional[np.ndarray] = None, stream=None) -> None:
+        """Rebuild the lost units in place (see plan_decode); the lost units'
+        current bytes are ignored."""
+        plan = self.plan_decode(parity, lost, stripes)
+        if plan is not None:
+            self.run(plan, stream)
 
     # ------------------------------------------------------------ update --
 
-    def update(self, parity: torch.Tensor, changed_units: Sequence[int],
-               old_units: Sequence[torch.Tensor], stream=None) -> None:
-        """Fold changed units into the parity in place:
+    def plan_update(self, parity: torch.Tensor, changed_units: Sequence[int],
+                    old_units: Sequence[torch.Tensor]) -> Optional[BatchPlan]:
+        """Descriptors for folding changed units into the parity:
         parity[s, i] ^= C[i][j] * (new ^ old) for each changed unit (s, j).
         ``changed_units`` are global unit indices (order of the layout) whose
-        new bytes are already in the tensors; ``old_units[n]`` holds the
-        previous bytes of ``changed_units[n]`` (at least its valid length)."""
+        new bytes are in the tensors when the plan runs; ``old_units[n]``
+        holds the previous bytes of ``changed_units[n]`` (at least its valid
+        length).  None if nothing changed."""
         k, m = self.k, self.m
         cu = np.asarray(changed_units, np.int64)
         if cu.size == 0:
-            return
+            return None
         if cu.size != len(old_units):
             raise ValueError("one old unit per changed unit")
         if np.unique(cu).size != cu.size or cu.min() < 0 or cu.max() >= self.n_units:
@@ -171,17 +212,37 @@ class StripeLayout:
             nptr[r, j] = self.host_ptrs[stripe[n], j]
             optr[r, j] = p
             ln[r, j] = self.host_len[stripe[n], j]
+        self._parity_ptrs_check(parity)
         pb = np.uint64(parity.data_ptr())
-        self._parity_ptrs(parity)
         pptr = (pb + (st.astype(np.uint64)[:, None] * np.uint64(m)
                       + np.arange(m, dtype=np.uint64)[None, :]) * np.uint64(self.unit_bytes))
-        dev = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).view(dt).copy()).to(self.device)
-        d_n, d_o, d_l, d_p = dev(nptr, np.int64), dev(optr, np.int64), dev(ln, np.int32), dev(pptr, np.int64)
-        _lib.check(_lib.lib().ec_parity_update(
-            _lib.u8ptr(self.coeff), k, m, d_n.data_ptr(), d_o.data_ptr(), d_l.data_ptr(),
-            d_p.data_ptr(), int(st.size), self.unit_bytes, stream_handle(stream)),
-            "ec_parity_update")
-        _hold(stream, d_n, d_o, d_l, d_p)
+        return BatchPlan("update", self.coeff, m, int(st.size),
+                         (self._to_dev(nptr, np.int64), self._to_dev(optr, np.int64),
+                          self._to_dev(ln, np.int32), self._to_dev(pptr, np.int64)))
+
+    def update(self, parity: torch.Tensor, changed_units: Sequence[int],
+               old_units: Sequence[torch.Tensor], stream=None) -> None:
+        """Fold changed units into the parity in place (see plan_update)."""
+        plan = self.plan_update(parity, changed_units, old_units)
+        if plan is not None:
+            self.run(plan, stream)
+
+    # --------------------------------------------------------------- run --
+
+    def run(self, plan: "BatchPlan", stream=None) -> None:
+        """Launch a decode or update plan (one kernel launch)."""
+        a, b, c, d = plan.desc
+        if plan.kind == "decode":
+            st = _lib.lib().ec_decode_batched(
+                _lib.u8ptr(plan.rows), self.k, plan.outputs, a.data_ptr(), b.data_ptr(),
+                c.data_ptr(), d.data_ptr(), plan.n_stripes, self.unit_bytes, stream_handle(stream))
+            _lib.check(st, "ec_decode_batched")
+        else:
+            st = _lib.lib().ec_parity_update(
+                _lib.u8ptr(plan.rows), self.k, self.m, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                d.data_ptr(), plan.n_stripes, self.unit_bytes, stream_handle(stream))
+            _lib.check(st, "ec_parity_update")
+        _hold(stream, a, b, c, d)
 
     # ----------------------------------------------------------- helpers --
 

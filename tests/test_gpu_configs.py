@@ -1,0 +1,165 @@
+"""The five BASELINE.json configurations at full size on the GPU.
+
+Bit-exact comparisons against the CPU encoder (oracle/ec_cpu_fast.c, itself
+pinned to the scalar oracle by test_oracle.py) where the bytes fit a host
+check in seconds; otherwise size-independent properties over the whole
+buffer (erase -> decode round trips, update == full re-encode) plus
+bit-exact checks of sampled stripes.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+MiB = 1 << 20
+THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def _say(msg):
+    print(f"[configs] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def synth(pkg):
+    from megatron_lm_amd import synth
+    return synth
+
+
+def test_config1_xor_4x64MiB(pkg, dev, synth):
+    _say("config 1: XOR 4 x 64 MiB bf16")
+    for seed in (0, 1):
+        host = synth.xor_shards(seed, 64 * MiB, 4)
+        p = pkg.xor_encode([torch.from_numpy(h).to(dev) for h in host])
+        torch.cuda.synchronize()
+        assert np.array_equal(p.cpu().numpy(), oracle.fast_xor_encode(host, nthreads=THREADS))
+
+
+@pytest.fixture(scope="module")
+def rs63(pkg, dev, synth):
+    _say("config 2: RS(6,3) 6 x 256 MiB fp32 optimizer state")
+    host = synth.rs_shards(0, 256 * MiB, 6)
+    data = [torch.from_numpy(h).to(dev) for h in host]
+    parity = pkg.rs_encode(data, 3)
+    torch.cuda.synchronize()
+    return host, data, parity
+
+
+def test_config2_rs63_256MiB_bit_exact(pkg, rs63):
+    host, data, parity = rs63
+    want = oracle.fast_rs_encode(oracle.cauchy(6, 3), host, nthreads=THREADS)
+    for i in range(3):
+        assert np.array_equal(parity[i].cpu().numpy(), want[i]), f"parity {i}"
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4])
+def test_config3_decode_three_erasures(pkg, rs63, synth, seed):
+    _, data, parity = rs63
+    cw = data + parity
+    lost = synth.erasures(seed, 9, 3)
+    _say(f"config 3: seed {seed} lost {lost}")
+    # The lost shards are zeroed and marked lost; the survivors are untouched.
+    work = [torch.zeros_like(t) if g in lost else t for g, t in enumerate(cw)]
+    rec = pkg.reconstruct([None if g in lost else t for g, t in enumerate(work)], 6, 3)
+    torch.cuda.synchronize()
+    for g in lost:
+        assert torch.equal(rec[g], cw[g]), f"shard {g}"
+
+
+def _check_sampled_stripes(layout, parity, stripes):
+    """Bit-exact check of the given stripes against the CPU encoder on host
+    copies of their zero-padded units."""
+    k, m, unit = layout.k, layout.m, layout.unit_bytes
+    for s in stripes:
+        units = []
+        for j in range(k):
+            buf = np.zeros(unit, np.uint8)
+            u = s * k + j
+            if u < layout.n_units:
+                v = layout.unit_view(u).cpu().numpy()
+                buf[: v.size] = v
+            units.append(buf)
+        want = oracle.fast_rs_encode(layout.coeff, units, nthreads=THREADS)
+        got = parity[s].cpu().numpy()
+        for i in range(m):
+            assert np.array_equal(got[i], want[i]), f"stripe {s} parity {i}"
+
+
+def test_config4_gpt13b_rank_buffer_rs82(pkg, dev, synth):
+    _say("config 4: 20.8 GB rank buffer, RS(8,2), 4 MiB units")
+    buf = synth.gpt_rank_buffer(dev, seed=4)
+    pset = pkg.encode([buf], 8, 2, 4 * MiB)
+    lay = pset.layout
+    assert lay.n_stripes == -(-buf.numel() // (8 * 4 * MiB))
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(4)
+    sample = sorted(set(rng.choice(lay.n_stripes, 12, replace=False).tolist()) | {lay.n_stripes - 1})
+    _say(f"config 4: {lay.n_stripes} stripes; checking {len(sample)} against the CPU encoder")
+    _check_sampled_stripes(lay, pset.parity, sample)
+    # Round trip over every stripe: lose one data and one parity position.
+    lost = [int(rng.integers(0, 8)), 8 + int(rng.integers(0, 2))]
+    ref_buf, ref_par = buf.clone(), pset.parity.clone()
+    view = buf.view(-1)
+    nfull = buf.numel() // (4 * MiB)
+    for s in range(lay.n_stripes):
+        u = s * 8 + lost[0]
+        if u < lay.n_units:
+            lay.unit_view(u).fill_(0)
+    pset.parity[:, lost[1] - 8].fill_(0)
+    pkg.decode(pset, lost)
+    torch.cuda.synchronize()
+    assert torch.equal(view, ref_buf) and torch.equal(pset.parity, ref_par), f"lost {lost}"
+    _say(f"config 4: round trip with lost {lost} ok ({nfull} full units)")
+
+
+def test_config5_ragged_3000_rs124_and_update(pkg, dev, synth):
+    _say("config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units")
+    sizes, kinds = synth.ragged_sizes(5)
+    tensors = []
+    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
+        dt = torch.bfloat16 if kind == 0 else torch.float32
+        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
+        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
+        tensors.append(t)
+    pset = pkg.encode(tensors, 12, 4, 64 << 10)
+    lay = pset.layout
+    _say(f"config 5: {lay.data_bytes / 1e9:.2f} GB in {lay.n_units} units, {lay.n_stripes} stripes")
+    rng = np.random.default_rng(5)
+    sample = sorted(set(rng.choice(lay.n_stripes, 24, replace=False).tolist()) | {lay.n_stripes - 1})
+    torch.cuda.synchronize()
+    _check_sampled_stripes(lay, pset.parity, sample)
+    # Incremental update after a seeded 1% perturbation == full re-encode.
+    changed = synth.perturbed_units(5, lay.n_units, 0.01)
+    olds = []
+    for u in changed.tolist():
+        v = lay.unit_view(u)
+        olds.append(v.clone())
+        v.copy_(torch.randint(0, 256, (v.numel(),), dtype=torch.uint8, device=dev))
+    pkg.update(pset, changed, olds)
+    fresh = lay.encode()
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity, fresh)
+    _say(f"config 5: update of {changed.size} units == re-encode")
+    # Round trip: lose 4 positions (2 data, 2 parity) of every stripe.
+    lost = sorted(rng.choice(12, 2, replace=False).tolist() + (12 + rng.choice(4, 2, replace=False)).tolist())
+    refs = [t.clone() for t in tensors]
+    ref_par = pset.parity.clone()
+    for s in range(lay.n_stripes):
+        for pos in lost:
+            u = s * 12 + pos
+            if pos < 12 and u < lay.n_units:
+                lay.unit_view(u).fill_(0)
+    for pos in lost:
+        if pos >= 12:
+            pset.parity[:, pos - 12].fill_(0)
+    pkg.decode(pset, lost)
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity, ref_par)
+    for t, r in zip(tensors, refs):
+        # byte compare: the perturbation wrote random bits, so floats may be NaN
+        assert torch.equal(t.view(-1).view(torch.uint8), r.view(-1).view(torch.uint8))
+    _say(f"config 5: round trip with lost {lost} ok")
