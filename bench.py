@@ -124,13 +124,7 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
     torch.cuda.empty_cache()
 
     # config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units, 1% update
-    sizes, kinds = synth.ragged_sizes(seed)
-    tensors = []
-    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
-        dt = torch.bfloat16 if kind == 0 else torch.float32
-        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
-        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
-        tensors.append(t)
+    tensors = ragged_tensors(synth, dev, seed)
     lay = pkg.StripeLayout(tensors, 12, 4, 64 << 10)
     par = lay.alloc_parity()
     w, e = timed(lambda: lay.encode(par), 10, 2)
@@ -169,6 +163,41 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
     del tensors, lay, par, olds, plan, dplan
     torch.cuda.empty_cache()
     return out
+
+
+def ragged_tensors(synth, dev, seed: int):
+    """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB)."""
+    import torch
+    sizes, kinds = synth.ragged_sizes(seed)
+    tensors = []
+    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
+        dt = torch.bfloat16 if kind == 0 else torch.float32
+        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
+        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
+        tensors.append(t)
+    return tensors
+
+
+def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
+    """Counter-run workload for the batched launcher: the 256 MiB streaming
+    copy (calibration, 3 launches) then 3 launches of the config-5 encode."""
+    import torch
+    shard = 256 * MiB
+    src = torch.empty(shard, dtype=torch.uint8, device=dev).random_(0, 256)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        pkg.xor_encode([src], out=dst)
+    torch.cuda.synchronize()
+    lay = pkg.StripeLayout(ragged_tensors(synth, dev, seed), 12, 4, 64 << 10)
+    par = lay.alloc_parity()
+    for _ in range(3):
+        lay.encode(par)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "batched-pmc", "copy_bytes_read": shard,
+                      "copy_bytes_written": shard, "data_bytes": lay.data_bytes,
+                      "parity_bytes": par.numel(), "n_units": lay.n_units,
+                      "n_stripes": lay.n_stripes}), flush=True)
+    return 0
 
 
 def measured_traffic(k: int, m: int, shard: int):
@@ -221,10 +250,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
-    ap.add_argument("--mode", choices=["full", "headline", "pmc"], default="full",
+    ap.add_argument("--mode", choices=["full", "headline", "pmc", "batched", "batched-pmc"],
+                    default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
-                         "plain 256 MiB copy and of the RS(6,3) encode, for counter runs")
+                         "plain 256 MiB copy and of the RS(6,3) encode, for counter runs; "
+                         "batched: configs 4 and 5 only; batched-pmc: the copy plus 3 "
+                         "launches of the config-5 encode, for counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the erasure-coding path has no multi-GPU "
@@ -242,6 +274,12 @@ def main() -> int:
 
     if args.mode == "pmc":
         return pmc_launches(pkg, dev)
+    if args.mode == "batched":
+        print(json.dumps({"mode": "batched", **batched_configs(pkg, synth, dev, args.seed)}),
+              flush=True)
+        return 0
+    if args.mode == "batched-pmc":
+        return batched_pmc_launches(pkg, synth, dev, args.seed)
 
     # ---- config 2: RS(6,3), 6 x 256 MiB fp32 optimizer state -------------
     k, m, shard = 6, 3, 256 * MiB
