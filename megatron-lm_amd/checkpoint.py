@@ -1,0 +1,468 @@
+"""Erasure-coded local checkpoints: the ``repl_strategy`` slot, filled with a code.
+
+The reference hands one rank's ``MCoreTensorAwareStateDict`` to an external
+``LocalCheckpointManager(root, repl_strategy=...)``:
+
+* construction, with ``CliqueReplicationStrategy`` as the redundancy policy:
+  megatron/training/training.py:825-835;
+* ``manager.save(tasd, iteration, is_async)``: megatron/training/checkpointing.py:538-541;
+* ``manager.find_latest()``: megatron/training/checkpointing.py:864;
+* ``manager.load() -> (tasd, name)``: megatron/training/checkpointing.py:891-894.
+
+Its tests pin what the slot must do: per-rank files ``iter_{:07d}_{rank}_local*``
+under ``root/<rank>/`` (tests/unit_tests/dist_checkpointing/test_replication.py:141-143);
+loading iteration 1 after the local directories of some ranks were deleted
+(:146-160); a failed save on one rank raising and loading nothing (test_local.py:246-326);
+saving iteration 2 removing iteration 1 (test_local.py:225-244).
+
+``ECLocalCheckpointManager`` keeps those call-site names and semantics.
+``ErasureCodedStrategy`` replaces full replicas with an (k, m) erasure code over
+each rank's ordered tensor list:
+
+* the rank's tensors are cut into stripes of k units of ``unit_bytes``
+  (``StripeLayout``) and m parity units are computed on the GPU;
+* codeword position p (data 0..k-1, parity k..k+m-1) of rank r's stripes is
+  a *slice* of n_stripes * unit_bytes bytes held by group rank (r + p) mod G,
+  so the storage of any m ranks can be lost and every rank still decodes
+  (G >= k + m);
+* storage is (k + m) / k of the data per rank, and a save moves
+  (k + m - 1) / k of it over the network.  Replication with factor F stores
+  F times the data and tolerates F - 1 losses.
+
+Slices are exchanged over the group's ``torch.distributed`` backend with CPU
+tensors (send/recv), and files are written as a JSON header plus raw bytes:
+nothing is pickled.  The GPU work (encode, gather of units into slices,
+scatter and reconstruction on load) goes through the engine's C ABI; the
+``codec`` argument exists so the exchange can be tested without a GPU.
+"""
+from __future__ import annotations
+
+import json
+import os
+import re
+import threading
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+import torch.distributed as dist
+
+GENERATOR_ID = "gf256-0x11d-cauchy1"
+_MAGIC = b"ECMI355\x00"
+_NAME_RE = re.compile(r"^iter_(\d{7})_(\d+)_local\.ec(\d+)$")
+
+
+class CheckpointingException(RuntimeError):
+    """A save or load that did not complete on every rank of the group."""
+
+
+# ----------------------------------------------------------------- state --
+
+@dataclass
+class TensorListState:
+    """The part of a tensor-aware state dict the redundancy step sees: an
+    ordered list of tensors (MCoreTensorAwareStateDict.tensors order,
+    megatron/core/dist_checkpointing/tensor_aware_state_dict.py:162-184) and
+    a JSON-able ``common`` dict that travels with them."""
+    tensors: List[torch.Tensor]
+    common: dict = field(default_factory=dict)
+
+    def pop_tensors(self) -> List[torch.Tensor]:
+        t, self.tensors = self.tensors, []
+        return t
+
+    def insert_tensors(self, tensors: Sequence[torch.Tensor]) -> None:
+        if self.tensors:
+            raise ValueError("state already holds tensors")
+        self.tensors = list(tensors)
+
+    @property
+    def is_hollow(self) -> bool:
+        return not self.tensors
+
+
+def _tensor_meta(tensors: Sequence[torch.Tensor]) -> list:
+    return [{"dtype": str(t.dtype).replace("torch.", ""), "shape": list(t.shape),
+             "nbytes": t.numel() * t.element_size()} for t in tensors]
+
+
+def _dtype(name: str) -> torch.dtype:
+    dt = getattr(torch, name, None)
+    if not isinstance(dt, torch.dtype):
+        raise CheckpointingException(f"unknown dtype {name!r} in checkpoint header")
+    return dt
+
+
+# ----------------------------------------------------------------- codec --
+
+class GpuSliceCodec:
+    """Encode a rank's tensors into k + m slices and back, on the GPU.
+
+    Slice p is the concatenation over stripes of unit p (zero-padded to
+    ``unit_bytes``), as n_stripes * unit_bytes host bytes.  Gathering units
+    into a slice and scattering them back are one launch each of the batched
+    kernels with k = m = 1 and coefficient 1 (a copy)."""
+
+    def __init__(self, k: int, m: int, unit_bytes: int):
+        from . import layout as _layout
+        self._layout = _layout
+        self.k, self.m, self.unit_bytes = k, m, unit_bytes
+
+    def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
+        from . import _lib
+        from .codec import stream_handle
+        lay = self._layout.StripeLayout(tensors, self.k, self.m, self.unit_bytes)
+        parity = lay.encode()
+        S, U = lay.n_stripes, self.unit_bytes
+        slices_dev = torch.empty((self.k, S, U), dtype=torch.uint8, device=lay.device)
+        one = np.ones((1, 1), np.uint8)
+        for p in range(self.k):
+            dptr = torch.from_numpy(np.ascontiguousarray(lay.host_ptrs[:, p]).view(np.int64)).to(lay.device)
+            dlen = torch.from_numpy(np.ascontiguousarray(lay.host_len[:, p]).view(np.int32)).to(lay.device)
+            base = np.uint64(slices_dev[p].data_ptr())
+            optr = torch.from_numpy((base + np.arange(S, dtype=np.uint64) * np.uint64(U))
+                                    .view(np.int64)).to(lay.device)
+            _lib.check(_lib.lib().ec_encode_batched(
+                _lib.u8ptr(one), 1, 1, dptr.data_ptr(), dlen.data_ptr(), optr.data_ptr(), S, U,
+                stream_handle()), "ec_encode_batched (gather)")
+        host = [slices_dev[p].cpu().numpy().reshape(-1) for p in range(self.k)]
+        host += [parity[:, i].contiguous().cpu().numpy().reshape(-1) for i in range(self.m)]
+        meta = {"k": self.k, "m": self.m, "unit_bytes": U, "n_stripes": S,
+                "n_units": lay.n_units, "tensors": _tensor_meta(tensors),
+                "generator": GENERATOR_ID}
+        return meta, host
+
+    def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
+        from . import _lib
+        from .codec import stream_handle
+        k, m, U, S = meta["k"], meta["m"], meta["unit_bytes"], meta["n_stripes"]
+        tensors = [torch.empty(tm["shape"], dtype=_dtype(tm["dtype"]), device=device)
+                   for tm in meta["tensors"]]
+        lay = self._layout.StripeLayout(tensors, k, m, U)
+        if lay.n_stripes != S or lay.n_units != meta["n_units"]:
+            raise CheckpointingException("checkpoint header does not match its tensors")
+        if len(slices) < k:
+            raise CheckpointingException(f"only {len(slices)} of the {k} slices needed")
+        parity = lay.alloc_parity()
+        parity.zero_()
+        one = np.ones((1, 1), np.uint8)
+        for p, buf in slices.items():
+            dev = torch.from_numpy(np.ascontiguousarray(buf)).to(device).view(S, U)
+            if p >= k:
+                parity[:, p - k].copy_(dev)
+                continue
+            sptr = torch.from_numpy((np.uint64(dev.data_ptr()) + np.arange(S, dtype=np.uint64)
+                                     * np.uint64(U)).view(np.int64)).to(device)
+            slen = torch.full((S,), U, dtype=torch.int32, device=device)
+            optr = torch.from_numpy(np.ascontiguousarray(lay.host_ptrs[:, p]).view(np.int64)).to(device)
+            olen = torch.from_numpy(np.ascontiguousarray(lay.host_len[:, p]).view(np.int32)).to(device)
+            # The temporaries are freed after the launch; the caching allocator
+            # orders their reuse after it on this stream.
+            _lib.check(_lib.lib().ec_decode_batched(
+                _lib.u8ptr(one), 1, 1, sptr.data_ptr(), slen.data_ptr(), optr.data_ptr(),
+                olen.data_ptr(), S, U, stream_handle()), "ec_decode_batched (scatter)")
+        lost = [p for p in range(k + m) if p not in slices]
+        if any(p < k for p in lost):
+            lay.decode(parity, lost)
+        torch.cuda.current_stream().synchronize()
+        return tensors
+
+
+# -------------------------------------------------------------- strategy --
+
+class ErasureCodedStrategy:
+    """(k, m) erasure code over each rank's tensors, slices placed on the
+    next k + m - 1 ranks of the group (see module docstring)."""
+
+    def __init__(self, k: int, m: int, unit_bytes: int = 4 << 20,
+                 group: Optional[dist.ProcessGroup] = None, codec=None):
+        if k < 1 or m < 1:
+            raise ValueError("k and m must be positive")
+        self.k, self.m, self.unit_bytes = k, m, unit_bytes
+        self.group = group
+        self.codec = codec if codec is not None else GpuSliceCodec(k, m, unit_bytes)
+
+    # group helpers
+    def ranks(self) -> List[int]:
+        if self.group is None:
+            return list(range(dist.get_world_size()))
+        return dist.get_process_group_ranks(self.group)
+
+    def holder(self, owner: int, pos: int) -> int:
+        r = self.ranks()
+        return r[(r.index(owner) + pos) % len(r)]
+
+    def check_group(self) -> None:
+        if len(self.ranks()) < self.k + self.m:
+            raise CheckpointingException(
+                f"group of {len(self.ranks())} ranks cannot hold k + m = {self.k + self.m} "
+                f"distinct slices")
+
+    def _exchange(self, outgoing: Dict[Tuple[int, int, int], np.ndarray],
+                  incoming: List[Tuple[int, int, int, int]]) -> Dict[Tuple[int, int, int], np.ndarray]:
+        """Point-to-point exchange.  outgoing[(dst, owner, pos)] = bytes to send;
+        incoming = [(src, owner, pos, nbytes)] to receive.  Every rank passes
+        the lists the plan gives it; transfers are ordered by (owner, pos) so
+        that both sides agree on tags."""
+        me = dist.get_rank()
+        reqs, recv = [], {}
+        for (src, owner, pos, n) in sorted(incoming, key=lambda x: (x[1], x[2])):
+            if src == me:
+                continue
+            buf = torch.empty(n, dtype=torch.uint8)
+            recv[(src, owner, pos)] = buf
+            reqs.append(dist.irecv(buf, src=src, group=self.group, tag=owner * 4096 + pos))
+        for (dst, owner, pos), data in sorted(outgoing.items(), key=lambda x: (x[0][1], x[0][2])):
+            if dst == me:
+                continue
+            reqs.append(dist.isend(torch.from_numpy(np.ascontiguousarray(data)), dst=dst,
+                                   group=self.group, tag=owner * 4096 + pos))
+        for r in reqs:
+            r.wait()
+        return {key: v.numpy() for key, v in recv.items()}
+
+
+def _pack(header: dict, payload: np.ndarray) -> np.ndarray:
+    h = json.dumps(header, sort_keys=True).encode()
+    out = np.empty(len(_MAGIC) + 8 + len(h) + payload.size, np.uint8)
+    out[: len(_MAGIC)] = np.frombuffer(_MAGIC, np.uint8)
+    out[len(_MAGIC): len(_MAGIC) + 8] = np.frombuffer(np.uint64(len(h)).tobytes(), np.uint8)
+    out[len(_MAGIC) + 8: len(_MAGIC) + 8 + len(h)] = np.frombuffer(h, np.uint8)
+    out[len(_MAGIC) + 8 + len(h):] = payload
+    return out
+
+
+def _unpack(blob: np.ndarray) -> Tuple[dict, np.ndarray]:
+    if bytes(blob[: len(_MAGIC)]) != _MAGIC:
+        raise CheckpointingException("not an erasure-coded checkpoint slice")
+    n = int(np.frombuffer(bytes(blob[len(_MAGIC): len(_MAGIC) + 8]), np.uint64)[0])
+    start = len(_MAGIC) + 8
+    header = json.loads(bytes(blob[start: start + n]).decode())
+    return header, blob[start + n:]
+
+
+# --------------------------------------------------------------- manager --
+
+class ECLocalCheckpointManager:
+    """Local (non-persistent) checkpoint manager with erasure-coded
+    redundancy, called like the reference's LocalCheckpointManager:
+    ``save(state, iteration, is_async)``, ``find_latest()``, ``load()``."""
+
+    def __init__(self, root_dir, repl_strategy: ErasureCodedStrategy):
+        self.root = Path(root_dir)
+        self.strategy = repl_strategy
+        self.rank = dist.get_rank()
+        self.latest_iteration = -1
+        self._pending: Optional[threading.Thread] = None
+
+    # paths
+    @property
+    def local_dir(self) -> Path:
+        return self.root / str(self.rank)
+
+    def _ckpt_id(self, iteration: int, owner: Optional[int] = None) -> str:
+        return f"iter_{iteration:07d}_{self.rank if owner is None else owner}_local"
+
+    def _slice_path(self, iteration: int, owner: int, pos: int) -> Path:
+        return self.local_dir / f"{self._ckpt_id(iteration, owner)}.ec{pos}"
+
+    def _inventory(self) -> Dict[int, List[Tuple[int, int, int]]]:
+        """{iteration: [(owner, pos, nbytes)]} of slices in this rank's dir."""
+        inv: Dict[int, List[Tuple[int, int, int]]] = {}
+        if self.local_dir.is_dir():
+            for f in self.local_dir.iterdir():
+                mt = _NAME_RE.match(f.name)
+                if mt:
+                    inv.setdefault(int(mt.group(1)), []).append(
+                        (int(mt.group(2)), int(mt.group(3)), f.stat().st_size))
+        return inv
+
+    # save
+    def save(self, state, iteration: int, is_async: bool = False):
+        """Encode this rank's tensors, place the k + m slices on their holders
+        and write them.  Collective over the strategy's group.  Raises
+        CheckpointingException on every rank if any rank fails; then no slice
+        of this iteration is left behind.  With is_async the GPU work and the
+        exchange still run here (no GPU work may move to a writer process);
+        only the file writes go to a thread, and the returned handle's
+        ``wait()`` finishes them."""
+        self.wait()
+        st = self.strategy
+        st.check_group()
+        me = self.rank
+        error = None
+        received: Dict[Tuple[int, int, int], np.ndarray] = {}
+        try:
+            tensors = state.tensors if hasattr(state, "tensors") else list(state)
+            common = getattr(state, "common", {})
+            meta, slices = st.codec.encode(tensors)
+            meta["common"] = common
+            meta["owner"] = me
+            meta["iteration"] = iteration
+            blobs = {p: _pack({**meta, "pos": p}, s) for p, s in enumerate(slices)}
+            sizes = torch.tensor([blobs[p].size for p in range(st.k + st.m)], dtype=torch.int64)
+        except Exception as e:  # noqa: BLE001 - reported collectively below
+            error = e
+            sizes = torch.full((st.k + st.m,), -1, dtype=torch.int64)
+        # every rank learns every blob size (and who failed)
+        ranks = st.ranks()
+        all_sizes = [torch.empty_like(sizes) for _ in ranks]
+        dist.all_gather(all_sizes, sizes, group=st.group)
+        failed = any(int(s[0]) < 0 for s in all_sizes)
+        if not failed:
+            outgoing = {(st.holder(me, p), me, p): blobs[p] for p in range(st.k + st.m)}
+            incoming = []
+            for owner, sz in zip(ranks, all_sizes):
+                for p in range(st.k + st.m):
+                    if st.holder(owner, p) == me:
+                        incoming.append((owner, owner, p, int(sz[p])))
+            got = st._exchange(outgoing, incoming)
+            for (src, owner, p), buf in got.items():
+                received[(owner, p)] = buf
+            for p in range(st.k + st.m):
+                if st.holder(me, p) == me:
+                    received[(me, p)] = blobs[p]
+
+        def write():
+            ok = True
+            try:
+                self.local_dir.mkdir(parents=True, exist_ok=True)
+                for (owner, p), blob in received.items():
+                    path = self._slice_path(iteration, owner, p)
+                    tmp = path.with_name(path.name + ".tmp")
+                    with open(tmp, "wb") as f:
+                        f.write(blob.tobytes())
+                    os.replace(tmp, path)
+            except Exception:  # noqa: BLE001
+                ok = False
+            return ok
+
+        if failed:
+            raise CheckpointingException(
+                f"erasure-coded save of iteration {iteration} failed on some rank") from error
+        if is_async:
+            handle = _AsyncSave(self, iteration, write)
+            self._pending = handle
+            handle.start()
+            return handle
+        ok = write()
+        self._finish_save(iteration, ok)
+        return None
+
+    def _finish_save(self, iteration: int, ok: bool) -> None:
+        flag = torch.tensor([0 if ok else 1], dtype=torch.int64)
+        dist.all_reduce(flag, group=self.strategy.group)
+        if int(flag[0]):
+            self._remove(lambda it: it == iteration)
+            raise CheckpointingException(f"writing iteration {iteration} failed on some rank")
+        self._remove(lambda it: it < iteration)
+        self.latest_iteration = iteration
+
+    def _remove(self, pred) -> None:
+        if not self.local_dir.is_dir():
+            return
+        for f in self.local_dir.iterdir():
+            mt = _NAME_RE.match(f.name)
+            if mt and pred(int(mt.group(1))):
+                f.unlink()
+
+    def wait(self) -> None:
+        if self._pending is not None:
+            h, self._pending = self._pending, None
+            h.wait()
+
+    # find / load
+    def _plan(self) -> Tuple[int, Dict[int, List[Tuple[int, int, int]]]]:
+        """Agree on the newest iteration every owner can decode, and for each
+        owner the k slices to read: {owner: [(holder, pos, nbytes)]}."""
+        st = self.strategy
+        inv = self._inventory()
+        gathered: List[dict] = [None] * len(st.ranks())
+        dist.all_gather_object(gathered, inv, group=st.group)
+        by_iter: Dict[int, Dict[int, Dict[int, Tuple[int, int]]]] = {}
+        for holder, hinv in zip(st.ranks(), gathered):
+            for it, entries in hinv.items():
+                for owner, pos, n in entries:
+                    if st.holder(owner, pos) != holder:
+                        continue  # stray file
+                    by_iter.setdefault(it, {}).setdefault(owner, {})[pos] = (holder, n)
+        for it in sorted(by_iter, reverse=True):
+            owners = by_iter[it]
+            if all(len(owners.get(o, {})) >= st.k for o in st.ranks()):
+                plan = {}
+                for o in st.ranks():
+                    avail = owners[o]
+                    chosen = sorted(avail)[: st.k]  # data positions first: no decode needed
+                    plan[o] = [(avail[p][0], p, avail[p][1]) for p in chosen]
+                return it, plan
+        return -1, {}
+
+    def find_latest(self) -> int:
+        self.wait()
+        it, _ = self._plan()
+        self.latest_iteration = it
+        return it
+
+    def load(self) -> Tuple[TensorListState, str]:
+        """Read back the newest iteration all ranks can decode, rebuilding this
+        rank's lost slices from any k of its k + m.  Collective."""
+        self.wait()
+        st = self.strategy
+        it, plan = self._plan()
+        if it < 0:
+            raise CheckpointingException("no erasure-coded checkpoint can be decoded")
+        me = self.rank
+        outgoing, incoming, local = {}, [], {}
+        for owner, reads in plan.items():
+            for holder, pos, n in reads:
+                if holder == me:
+                    blob = np.fromfile(self._slice_path(it, owner, pos), dtype=np.uint8)
+                    if owner == me:
+                        local[pos] = blob
+                    else:
+                        outgoing[(owner, owner, pos)] = blob
+                if owner == me and holder != me:
+                    incoming.append((holder, owner, pos, n))
+        got = st._exchange(outgoing, incoming)
+        blobs = dict(local)
+        for (src, owner, pos), buf in got.items():
+            blobs[pos] = buf
+        slices, meta = {}, None
+        for pos, blob in blobs.items():
+            header, payload = _unpack(blob)
+            if header.get("owner") != me or header.get("iteration") != it or header.get("pos") != pos:
+                raise CheckpointingException("slice header does not match its name")
+            if header.get("generator") != GENERATOR_ID:
+                raise CheckpointingException(f"unknown generator {header.get('generator')!r}")
+            meta = header
+            slices[pos] = payload
+        device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else torch.device("cpu")
+        tensors = st.codec.decode(meta, slices, device)
+        self.latest_iteration = it
+        return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
+
+
+class _AsyncSave:
+    """Handle of an asynchronous save: file writes on a thread; ``wait()``
+    joins it and runs the collective success check."""
+
+    def __init__(self, mgr: ECLocalCheckpointManager, iteration: int, write):
+        self.mgr, self.iteration, self.write = mgr, iteration, write
+        self.ok = False
+        self.thread = threading.Thread(target=self._run, daemon=True)
+        self.done = False
+
+    def _run(self):
+        self.ok = self.write()
+
+    def start(self):
+        self.thread.start()
+
+    def wait(self):
+        if self.done:
+            return
+        self.thread.join()
+        self.done = True
+        self.mgr._finish_save(self.iteration, self.ok)

@@ -1,0 +1,115 @@
+"""Per-rank scenarios of the erasure-coded checkpoint manager, run in spawned
+processes by test_checkpoint_cpu.py (gloo) and test_gpu_checkpoint.py."""
+import os
+import shutil
+import sys
+import traceback
+
+import torch
+import torch.distributed as dist
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def make_tensors(rank, device="cpu"):
+    g = torch.Generator().manual_seed(100 + rank)
+    sizes = [(3, 1000), (17,), (257, 33), (1,), (4096,), (5, 7, 11)]
+    dts = [torch.float32, torch.bfloat16, torch.float32, torch.int64, torch.uint8, torch.float16]
+    out = []
+    for shp, dt in zip(sizes[: 3 + rank % 4], dts):
+        x = torch.randn(shp, generator=g).to(dt) if dt.is_floating_point else \
+            torch.randint(0, 200, shp, generator=g).to(dt)
+        out.append(x.to(device))
+    return out
+
+
+def same(a, b):
+    return len(a) == len(b) and all(
+        x.dtype == y.dtype and x.shape == y.shape and
+        torch.equal(x.cpu().reshape(-1).view(torch.uint8), y.cpu().reshape(-1).view(torch.uint8))
+        for x, y in zip(a, b))
+
+
+def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile):
+    try:
+        sys.path.insert(0, ROOT)
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        os.environ["MASTER_ADDR"] = "127.0.0.1"
+        os.environ["MASTER_PORT"] = str(port)
+        dist.init_process_group("gloo", rank=rank, world_size=world)
+        import __graft_entry__
+        __graft_entry__.load_package()
+        from megatron_lm_amd.checkpoint import (CheckpointingException, ECLocalCheckpointManager,
+                                                ErasureCodedStrategy, TensorListState)
+        device = "cpu"
+        if use_gpu:
+            torch.cuda.set_device(0)
+            device = "cuda:0"
+            codec = None
+        else:
+            from ec_cpu_codec import OracleSliceCodec
+            codec = OracleSliceCodec(k, m, unit)
+        strat = ErasureCodedStrategy(k, m, unit, codec=codec)
+        mgr = ECLocalCheckpointManager(root, strat)
+        mine = make_tensors(rank, device)
+        state = TensorListState([t.clone() for t in mine], {"rank": rank})
+
+        if scenario == "recover":
+            mgr.save(state, 1)
+            dist.barrier()
+            names = sorted(f.name for f in mgr.local_dir.iterdir())
+            want = sorted(f"iter_0000001_{(rank - p) % world}_local.ec{p}" for p in range(k + m))
+            assert names == want, (names, want)
+            lost = [(world - 1) - 2 * i for i in range(m)]  # m ranks lose their storage
+            if rank in lost:
+                shutil.rmtree(mgr.local_dir)
+                os.makedirs(mgr.local_dir)
+            dist.barrier()
+            assert mgr.find_latest() == 1
+            got, name = mgr.load()
+            assert name == f"iter_0000001_{rank}_local", name
+            assert same(got.tensors, mine) and got.common == {"rank": rank}
+        elif scenario == "cleanup":
+            mgr.save(state, 1)
+            mgr.save(state, 2)
+            names = {f.name for f in mgr.local_dir.iterdir()}
+            assert not any(n.startswith("iter_0000001") for n in names), names
+            got, name = mgr.load()
+            assert name.startswith("iter_0000002") and same(got.tensors, mine)
+        elif scenario == "failed_save":
+            mgr.save(state, 1)
+            if rank == 1:
+                strat.codec = type(strat.codec)(k, m, unit, fail=True)
+            try:
+                mgr.save(state, 2)
+                raise AssertionError("save on a failing rank did not raise")
+            except CheckpointingException:
+                pass
+            names = {f.name for f in mgr.local_dir.iterdir()}
+            assert not any(n.startswith("iter_0000002") for n in names), names
+            assert mgr.find_latest() == 1
+        elif scenario == "too_many_lost":
+            mgr.save(state, 1)
+            dist.barrier()
+            if rank < m + 1:
+                shutil.rmtree(mgr.local_dir)
+            dist.barrier()
+            assert mgr.find_latest() == -1
+            try:
+                mgr.load()
+                raise AssertionError("load with more than m losses did not raise")
+            except CheckpointingException:
+                pass
+        elif scenario == "async":
+            h = mgr.save(state, 3, is_async=True)
+            h.wait()
+            got, _ = mgr.load()
+            assert same(got.tensors, mine)
+        else:
+            raise ValueError(scenario)
+        dist.barrier()
+        dist.destroy_process_group()
+    except BaseException:
+        with open(f"{errfile}.{rank}", "w") as f:
+            f.write(traceback.format_exc())
+        raise
