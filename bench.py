@@ -165,6 +165,51 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
     return out
 
 
+def overlap_with_training(pkg, dev, data, parity, coeff) -> dict:
+    """Checkpoint encode concurrent with a training-like load: 8192^3 bf16
+    GEMMs on torch's stream, the RS(6,3) encode on a side stream of default
+    priority.  Reports each one alone and both together (HIP events on each
+    stream), so the interference on training is visible."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16, generator=g)
+    b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16, generator=g)
+    c = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
+    side = torch.cuda.Stream(device=dev)
+    n_gemm, n_enc = 30, 120
+
+    def run(do_gemm, do_enc):
+        main = torch.cuda.current_stream()
+        ev = {k: torch.cuda.Event(enable_timing=True) for k in ("g0", "g1", "e0", "e1")}
+        torch.cuda.synchronize()
+        if do_enc:
+            ev["e0"].record(side)
+            for _ in range(n_enc):
+                pkg.matvec(coeff, data, out=parity, stream=side)
+            ev["e1"].record(side)
+        if do_gemm:
+            ev["g0"].record(main)
+            for _ in range(n_gemm):
+                torch.matmul(a, b, out=c)
+            ev["g1"].record(main)
+        torch.cuda.synchronize()
+        return (ev["g0"].elapsed_time(ev["g1"]) / n_gemm if do_gemm else None,
+                ev["e0"].elapsed_time(ev["e1"]) / n_enc if do_enc else None)
+
+    run(True, True)  # warm-up of both
+    g_alone, _ = run(True, False)
+    _, e_alone = run(False, True)
+    g_both, e_both = run(True, True)
+    flops = 2 * 8192 ** 3
+    data_bytes = sum(t.numel() for t in data)
+    return {"overlap_gemm_ms_alone": round(g_alone, 3),
+            "overlap_gemm_ms_with_encode": round(g_both, 3),
+            "overlap_gemm_TFLOPs_alone": round(flops / g_alone / 1e9, 1),
+            "overlap_encode_GBps_alone": round(data_bytes / e_alone / 1e6, 1),
+            "overlap_encode_GBps_with_gemm": round(data_bytes / e_both / 1e6, 1)}
+
+
 def ragged_tensors(synth, dev, seed: int):
     """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB)."""
     import torch
@@ -243,8 +288,8 @@ def pmc_launches(pkg, dev) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -332,6 +377,9 @@ def main() -> int:
     log(f"XOR(4) {xor_gbs:.1f} GB/s data")
 
     batched = {} if args.no_batched else batched_configs(pkg, synth, dev, args.seed)
+    log("encode on a side stream vs bf16 GEMMs")
+    over = overlap_with_training(pkg, dev, data, parity, coeff)
+    log(f"overlap: {over}")
 
     # ---- practical ceiling: device-to-device copy -------------------------
     src = torch.empty(k * shard, dtype=torch.uint8, device=dev)
@@ -377,6 +425,7 @@ def main() -> int:
             "decode_kernel_us": round(dev_ms * 1e3, 2),
             "xor_4x64MiB_GBps": round(xor_gbs, 2), "xor_kernel_us": round(xev * 1e3, 2),
             **batched,
+            **over,
             "d2d_copy_GBps": round(copy_gbs, 1),
             "encode_frac_of_copy": round(enc_traffic_gbs / copy_gbs, 4),
         },

@@ -70,6 +70,22 @@ def test_config3_decode_three_erasures(pkg, rs63, synth, seed):
         assert torch.equal(rec[g], cw[g]), f"shard {g}"
 
 
+def test_config3_every_erasure_pattern_full_size(pkg, rs63):
+    """All 129 patterns of at most 3 lost shards among the 9, at full size."""
+    import itertools
+    _, data, parity = rs63
+    cw = data + parity
+    n = 0
+    for e in (1, 2, 3):
+        for lost in itertools.combinations(range(9), e):
+            rec = pkg.reconstruct([None if g in lost else t for g, t in enumerate(cw)], 6, 3)
+            torch.cuda.synchronize()
+            for g in lost:
+                assert torch.equal(rec[g], cw[g]), f"lost {lost} shard {g}"
+            n += 1
+    assert n == 129
+
+
 def _check_sampled_stripes(layout, parity, stripes):
     """Bit-exact check of the given stripes against the CPU encoder on host
     copies of their zero-padded units."""
