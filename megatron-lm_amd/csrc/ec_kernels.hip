@@ -527,45 +527,77 @@ struct UpdateArgs {
   const uint64_t* pptr;  // [n_stripes][M]
   PermTab tab[M][K];
   uint32_t unit_bytes;
-  uint32_t tiles_per_unit;
+  uint32_t tiles_per_unit;   // tiles of kBlock*16 bytes in a unit
+  uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
+  uint32_t blocks_per_unit;
 };
 
+// Incremental update: each workgroup walks a span of tiles of one changed
+// stripe.  The stripe's descriptors (which units changed, where their old
+// and new bytes are, their lengths) are read once per span into scalar
+// registers; a tile inside every changed unit, with everything 16-byte
+// aligned, takes plain vector loads, any other tile the byte-granular path.
 template <int K, int M>
 __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a) {
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
-  const uint32_t s = blockIdx.x / a.tiles_per_unit;
-  const uint32_t t = blockIdx.x - s * a.tiles_per_unit;
-  const uint32_t off = (t * kBlock + threadIdx.x) * 16u;
-  if (off >= a.unit_bytes) return;
-  uint32_t acc[M][4] = {};
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  const uint8_t* nw[K];
+  const uint8_t* od[K];
+  uint32_t len[K];
+  uint32_t full = a.unit_bytes;
+  bool aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    const uint8_t* nw = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
-    if (nw == nullptr) continue;  // uniform: unchanged unit
-    const uint8_t* od = reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]);
-    uint32_t l = a.len[(uint64_t)s * K + j];
-    l = l < a.unit_bytes ? l : a.unit_bytes;
-    if (off >= l) continue;
-    const uint4 vn = load_unit(nw, off, l);
-    const uint4 vo = load_unit(od, off, l);
-    const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
-    Fields f[4];
-#pragma unroll
-    for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(dl, dd));
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-      asm volatile("" ::: "memory");
-      const PermTab tj = tab[i][j];
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], tj, f[dd]);
+    nw[j] = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
+    od[j] = nw[j] ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]) : nullptr;
+    const uint32_t l = nw[j] ? a.len[(uint64_t)s * K + j] : 0u;
+    len[j] = l < a.unit_bytes ? l : a.unit_bytes;
+    if (nw[j]) {
+      full = len[j] < full ? len[j] : full;
+      aligned &= ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
     }
   }
+  uint8_t* p[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
-    const uint4 v = load_unit(p, off, a.unit_bytes);
-    store_unit(p, off, make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]));
+    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+  }
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t off = (t * kBlock + threadIdx.x) * 16u;
+    if (off >= a.unit_bytes) continue;
+    const bool fast = aligned && (t + 1) * (kBlock * 16u) <= full;
+    uint32_t acc[M][4] = {};
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      if (nw[j] == nullptr) continue;  // uniform: unchanged unit
+      if (!fast && off >= len[j]) continue;
+      const uint4 vn = fast ? load_stream(nw[j] + off) : load_unit(nw[j], off, len[j]);
+      const uint4 vo = fast ? load_stream(od[j] + off) : load_unit(od[j], off, len[j]);
+      const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
+      Fields f[4];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(dl, dd));
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        asm volatile("" ::: "memory");
+        const PermTab tj = tab[i][j];
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], tj, f[dd]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      const uint4 v = fast ? load_stream(p[i] + off) : load_unit(p[i], off, a.unit_bytes);
+      const uint4 w = make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]);
+      if (fast)
+        store_stream(p[i] + off, w);
+      else
+        store_unit(p[i], off, w);
+    }
   }
 }
 
@@ -660,7 +692,17 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
   a.tiles_per_unit = (unit16 + kBlock - 1) / kBlock;
-  const uint64_t blocks = (uint64_t)n_stripes * a.tiles_per_unit;
+  // Spans of up to 64 KiB per unit, keeping at least 16384 workgroups: each
+  // tile is a dependent chain (unit loads, then the parity read-modify-
+  // write), so the update needs more workgroups in flight than the encode.
+  uint64_t tpb = (64u << 10) / (kBlock * 16u);
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  if (total_tiles / tpb < 16384) tpb = total_tiles / 16384;
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
   hipLaunchKernelGGL((update_kernel<K, M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
   return hip_status();
