@@ -270,7 +270,9 @@ void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
                       const uint8_t* const* data, uint8_t* const* parity,
                       uint64_t n, int nthreads) {
   if (m > EC_ORACLE_MAX_M) return;
-  coef_tab* tabs = (coef_tab*)aligned_alloc(64, sizeof(coef_tab) * (size_t)(k * m) + 64);
+  /* aligned_alloc wants the size to be a multiple of the alignment */
+  const size_t bytes = (sizeof(coef_tab) * (size_t)(k * m) + 63) & ~(size_t)63;
+  coef_tab* tabs = (coef_tab*)aligned_alloc(64, bytes);
   for (int i = 0; i < m * k; ++i) make_tab(coeff[i], &tabs[i]);
   job base = {data, parity, tabs, k, m, 0, 0};
   run_threads(base, n, nthreads);

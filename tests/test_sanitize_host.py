@@ -1,0 +1,29 @@
+"""Host code under AddressSanitizer and UndefinedBehaviorSanitizer: the C
+oracle, the SIMD CPU encoder and the engine's host GF(2^8) code
+(megatron-lm_amd/csrc/gf256.cpp), built with gcc/g++ on their own (no device
+code) and driven by tests/sanitize_driver.c."""
+import os
+import subprocess
+
+from conftest import ROOT
+
+SAN = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", "-g", "-O1"]
+
+
+def test_host_code_is_sanitizer_clean(tmp_path):
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "oracle")]
+    objs = []
+    for src, cc, std in [(os.path.join(ROOT, "oracle", "ec_oracle.c"), "gcc", "-std=c11"),
+                         (os.path.join(ROOT, "oracle", "ec_cpu_fast.c"), "gcc", "-std=c11"),
+                         (os.path.join(ROOT, "megatron-lm_amd", "csrc", "gf256.cpp"), "g++", "-std=c++17"),
+                         (os.path.join(ROOT, "tests", "sanitize_driver.c"), "gcc", "-std=c11")]:
+        obj = str(tmp_path / (os.path.basename(src) + ".o"))
+        subprocess.run([cc, std, *SAN, *inc, "-c", src, "-o", obj], check=True)
+        objs.append(obj)
+    exe = str(tmp_path / "drv")
+    subprocess.run(["g++", *SAN, *objs, "-o", exe, "-pthread"], check=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="print_stacktrace=1")
+    env.pop("LD_PRELOAD", None)
+    out = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=300)
+    assert out.returncode == 0, out.stderr[-4000:]
+    assert "sanitize driver ok" in out.stdout
