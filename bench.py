@@ -160,9 +160,49 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
     w, e = timed(lambda: lay.run(dplan), 5, 1)
     out["rs124_ragged_decode4_GBps"] = round(lay.data_bytes / (e * 1e-3) / 1e9, 1)
     log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
-    del tensors, lay, par, olds, plan, dplan
+    del lay, par, olds, plan, dplan
+    torch.cuda.empty_cache()
+    out.update(checkpoint_staging(pkg, tensors))
+    del tensors
     torch.cuda.empty_cache()
     return out
+
+
+def checkpoint_staging(pkg, tensors) -> dict:
+    """The save and load sides of the erasure-coded checkpoint manager on one
+    GPU, for config 5's tensors: encode into k + m slices and stage them to
+    pinned host memory (one transfer), and back: k slices with two data
+    positions missing to rebuilt tensors.  Data GB/s over wall time; the
+    second call of each is timed (the first pins the host buffers)."""
+    import torch
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    codec = GpuSliceCodec(12, 4, 64 << 10)
+    nbytes = sum(t.numel() * t.element_size() for t in tensors)
+    try:
+        codec.encode(tensors)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        meta, slices = codec.encode(tensors)
+        t_enc = time.perf_counter() - t0
+        keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
+        keep = dict(list(sorted(keep.items()))[:12])
+        dev = tensors[0].device
+        del slices
+        codec.decode(meta, keep, dev)
+        t0 = time.perf_counter()
+        rebuilt = codec.decode(meta, keep, dev)
+        t_dec = time.perf_counter() - t0
+        ok = all(torch.equal(a.view(-1).view(torch.uint8), b.view(-1).view(torch.uint8))
+                 for a, b in zip(rebuilt, tensors))
+        if not ok:
+            raise AssertionError("checkpoint decode did not rebuild the tensors")
+        del rebuilt, keep
+        res = {"ckpt_encode_to_host_GBps": round(nbytes / t_enc / 1e9, 1),
+               "ckpt_decode_from_host_GBps": round(nbytes / t_dec / 1e9, 1)}
+    except RuntimeError as e:  # pinned-memory limits differ between hosts
+        res = {"ckpt_staging_error": str(e)[:200]}
+    log(f"checkpoint staging: {res}")
+    return res
 
 
 def overlap_with_training(pkg, dev, data, parity, coeff) -> dict:

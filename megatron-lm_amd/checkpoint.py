@@ -41,6 +41,7 @@ import json
 import os
 import re
 import threading
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -100,72 +101,116 @@ def _dtype(name: str) -> torch.dtype:
 class GpuSliceCodec:
     """Encode a rank's tensors into k + m slices and back, on the GPU.
 
-    Slice p is the concatenation over stripes of unit p (zero-padded to
-    ``unit_bytes``), as n_stripes * unit_bytes host bytes.  Gathering units
-    into a slice and scattering them back are one launch each of the batched
-    kernels with k = m = 1 and coefficient 1 (a copy)."""
+    Slice p is the concatenation over stripes of codeword position p (units
+    zero-padded to ``unit_bytes``): n_stripes * unit_bytes bytes.  Encode
+    builds all k + m slices in one device block (the parity kernel writes its
+    units straight into the parity slices, one gather launch copies the data
+    units into theirs) and moves the block to pinned host memory in one
+    transfer.  Decode moves the k slices it got back in one transfer, scatters
+    the data slices into fresh tensors in one launch, and rebuilds the lost
+    data positions from the k slices in one more.  The returned host slices
+    are views of one pinned buffer."""
 
     def __init__(self, k: int, m: int, unit_bytes: int):
         from . import layout as _layout
         self._layout = _layout
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
 
+    @staticmethod
+    def _rows(block: torch.Tensor, p: int) -> np.ndarray:
+        """Device addresses of the n_stripes units of slice p of a block."""
+        S, U = block.shape[1], block.shape[2]
+        return np.uint64(block[p].data_ptr()) + np.arange(S, dtype=np.uint64) * np.uint64(U)
+
+    @staticmethod
+    def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
+
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         from . import _lib
         from .codec import stream_handle
-        lay = self._layout.StripeLayout(tensors, self.k, self.m, self.unit_bytes)
-        parity = lay.encode()
-        S, U = lay.n_stripes, self.unit_bytes
-        slices_dev = torch.empty((self.k, S, U), dtype=torch.uint8, device=lay.device)
+        k, m, U = self.k, self.m, self.unit_bytes
+        lay = self._layout.StripeLayout(tensors, k, m, U)
+        S, dev = lay.n_stripes, lay.device
+        block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
+        # parity unit (s, i) goes to row s of slice k + i
+        pptr = np.stack([self._rows(block, k + i) for i in range(m)], axis=1)
+        pptr = self._dev(pptr, np.int64, dev)
+        _lib.check(_lib.lib().ec_encode_batched(
+            _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+            pptr.data_ptr(), S, U, stream_handle()), "ec_encode_batched")
+        # gather: every data unit (s, p) to row s of slice p, one k=m=1 launch
+        optr = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1), np.int64, dev)
         one = np.ones((1, 1), np.uint8)
-        for p in range(self.k):
-            dptr = torch.from_numpy(np.ascontiguousarray(lay.host_ptrs[:, p]).view(np.int64)).to(lay.device)
-            dlen = torch.from_numpy(np.ascontiguousarray(lay.host_len[:, p]).view(np.int32)).to(lay.device)
-            base = np.uint64(slices_dev[p].data_ptr())
-            optr = torch.from_numpy((base + np.arange(S, dtype=np.uint64) * np.uint64(U))
-                                    .view(np.int64)).to(lay.device)
-            _lib.check(_lib.lib().ec_encode_batched(
-                _lib.u8ptr(one), 1, 1, dptr.data_ptr(), dlen.data_ptr(), optr.data_ptr(), S, U,
-                stream_handle()), "ec_encode_batched (gather)")
-        host = [slices_dev[p].cpu().numpy().reshape(-1) for p in range(self.k)]
-        host += [parity[:, i].contiguous().cpu().numpy().reshape(-1) for i in range(self.m)]
-        meta = {"k": self.k, "m": self.m, "unit_bytes": U, "n_stripes": S,
-                "n_units": lay.n_units, "tensors": _tensor_meta(tensors),
-                "generator": GENERATOR_ID}
-        return meta, host
+        _lib.check(_lib.lib().ec_encode_batched(
+            _lib.u8ptr(one), 1, 1, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(), optr.data_ptr(),
+            S * k, U, stream_handle()), "ec_encode_batched (gather)")
+        host = torch.empty((k + m, S, U), dtype=torch.uint8, pin_memory=True)
+        host.copy_(block, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        meta = {"k": k, "m": m, "unit_bytes": U, "n_stripes": S, "n_units": lay.n_units,
+                "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
+        return meta, [host[p].numpy().reshape(-1) for p in range(k + m)]
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib
-        from .codec import stream_handle
+        from .codec import decode_matrix, stream_handle
         k, m, U, S = meta["k"], meta["m"], meta["unit_bytes"], meta["n_stripes"]
+        if len(slices) < k:
+            raise CheckpointingException(f"only {len(slices)} of the {k} slices needed")
+        avail = sorted(slices)[:k]
+        for p in avail:
+            if slices[p].size != S * U:
+                raise CheckpointingException(f"slice {p} has {slices[p].size} bytes, not {S * U}")
         tensors = [torch.empty(tm["shape"], dtype=_dtype(tm["dtype"]), device=device)
                    for tm in meta["tensors"]]
         lay = self._layout.StripeLayout(tensors, k, m, U)
         if lay.n_stripes != S or lay.n_units != meta["n_units"]:
             raise CheckpointingException("checkpoint header does not match its tensors")
-        if len(slices) < k:
-            raise CheckpointingException(f"only {len(slices)} of the {k} slices needed")
-        parity = lay.alloc_parity()
-        parity.zero_()
+        host = torch.empty((k, S, U), dtype=torch.uint8, pin_memory=True)
+        hv = host.numpy()
+        # Copy the slices into the pinned block in parallel pieces (numpy
+        # releases the GIL for large copies): one thread moves ~10 GB/s.
+        pieces = [(r, a, min(a + (64 << 20), S * U)) for r in range(k)
+                  for a in range(0, S * U, 64 << 20)]
+        flat = hv.reshape(k, -1)
+
+        def put(piece):
+            r, a, b = piece
+            flat[r, a:b] = slices[avail[r]][a:b]
+        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+            list(pool.map(put, pieces))
+        block = host.to(device, non_blocking=True)
         one = np.ones((1, 1), np.uint8)
-        for p, buf in slices.items():
-            dev = torch.from_numpy(np.ascontiguousarray(buf)).to(device).view(S, U)
-            if p >= k:
-                parity[:, p - k].copy_(dev)
-                continue
-            sptr = torch.from_numpy((np.uint64(dev.data_ptr()) + np.arange(S, dtype=np.uint64)
-                                     * np.uint64(U)).view(np.int64)).to(device)
-            slen = torch.full((S,), U, dtype=torch.int32, device=device)
-            optr = torch.from_numpy(np.ascontiguousarray(lay.host_ptrs[:, p]).view(np.int64)).to(device)
-            olen = torch.from_numpy(np.ascontiguousarray(lay.host_len[:, p]).view(np.int32)).to(device)
-            # The temporaries are freed after the launch; the caching allocator
-            # orders their reuse after it on this stream.
+        # scatter the data slices we have into the tensors, one k=m=1 launch
+        have = [(r, p) for r, p in enumerate(avail) if p < k]
+        if have:
+            sptr = np.concatenate([self._rows(block, r) for r, _ in have])
+            optr = np.concatenate([lay.host_ptrs[:, p] for _, p in have])
+            olen = np.concatenate([lay.host_len[:, p] for _, p in have])
+            args = [self._dev(sptr, np.int64, device),
+                    torch.full((sptr.size,), U, dtype=torch.int32, device=device),
+                    self._dev(optr, np.int64, device), self._dev(olen, np.int32, device)]
             _lib.check(_lib.lib().ec_decode_batched(
-                _lib.u8ptr(one), 1, 1, sptr.data_ptr(), slen.data_ptr(), optr.data_ptr(),
-                olen.data_ptr(), S, U, stream_handle()), "ec_decode_batched (scatter)")
-        lost = [p for p in range(k + m) if p not in slices]
-        if any(p < k for p in lost):
-            lay.decode(parity, lost)
+                _lib.u8ptr(one), 1, 1, *[t.data_ptr() for t in args], sptr.size, U,
+                stream_handle()), "ec_decode_batched (scatter)")
+        # rebuild the missing data positions from the k slices, one launch
+        lost_data = [p for p in range(k) if p not in slices or p not in avail]
+        if lost_data:
+            erased = [p for p in range(k + m) if p not in avail]
+            surv, rows = decode_matrix(lay.coeff, erased)
+            if surv != avail:
+                raise CheckpointingException("decode plan does not match the slices read")
+            pick = [erased.index(p) for p in lost_data]
+            rows = np.ascontiguousarray(rows[pick])
+            sptr = np.stack([self._rows(block, r) for r in range(k)], axis=1)
+            args = [self._dev(sptr, np.int64, device),
+                    torch.full((S, k), U, dtype=torch.int32, device=device),
+                    self._dev(lay.host_ptrs[:, lost_data], np.int64, device),
+                    self._dev(lay.host_len[:, lost_data], np.int32, device)]
+            _lib.check(_lib.lib().ec_decode_batched(
+                _lib.u8ptr(rows), k, len(lost_data), *[t.data_ptr() for t in args], S, U,
+                stream_handle()), "ec_decode_batched")
         torch.cuda.current_stream().synchronize()
         return tensors
 
