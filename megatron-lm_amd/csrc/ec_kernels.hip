@@ -637,8 +637,6 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
 
 // ---------------------------------------------------------- host launch --
 
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 inline int hip_status() { return hipGetLastError() == hipSuccess ? EC_OK : EC_EHIP; }
 
 // Grid for a grid-stride kernel over n16 chunks with U chunks per lane:
@@ -805,28 +803,47 @@ int launch_generic(const uint8_t* coeff, int k, int m, const uint8_t* const* d,
   return hip_status();
 }
 
+// Common misalignment of a set of addresses modulo 16, or -1 if they differ.
+inline int common_skew(const uint8_t* const* a, int n, int skew) {
+  for (int i = 0; i < n; ++i) {
+    const int s = (int)(reinterpret_cast<uintptr_t>(a[i]) & 15u);
+    if (skew < 0) skew = s;
+    else if (s != skew) return -1;
+  }
+  return skew;
+}
+
 int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t* const* o,
            uint64_t nbytes, hipStream_t st) {
   if (!coeff || !d || !o) return EC_EINVAL;
   if (k < 1 || m < 1) return EC_EINVAL;
   if (k > EC_MAX_K || m > EC_MAX_M) return EC_ERANGE;
-  bool aligned = true;
-  for (int j = 0; j < k; ++j) {
+  for (int j = 0; j < k; ++j)
     if (!d[j]) return EC_EINVAL;
-    aligned &= aligned16(d[j]);
-  }
-  for (int i = 0; i < m; ++i) {
+  for (int i = 0; i < m; ++i)
     if (!o[i]) return EC_EINVAL;
-    aligned &= aligned16(o[i]);
-  }
   if (nbytes == 0) return EC_OK;
-  if (!aligned || k > kFastMaxK || m > kFastMaxM)
+  // Shards misaligned by the same amount (equal-offset views) run the first
+  // bytes up to the next 16-byte boundary through the byte kernel and the
+  // rest through the vector kernel; different misalignments take the byte
+  // kernel throughout.
+  const int skew = common_skew(o, m, common_skew(d, k, -1));
+  if (skew < 0 || k > kFastMaxK || m > kFastMaxM)
     return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
-  const uint64_t n16 = nbytes / 16;
+  uint64_t head = skew ? 16u - (uint64_t)skew : 0;
+  if (head > nbytes) head = nbytes;
   int s = EC_OK;
-  if (n16) s = kRsTable[k - 1][m - 1](coeff, d, o, n16, st);
-  if (s == EC_OK && (nbytes & 15))
-    s = launch_generic(coeff, k, m, d, o, n16 * 16, nbytes & 15, st);
+  if (head) s = launch_generic(coeff, k, m, d, o, 0, head, st);
+  const uint64_t n16 = (nbytes - head) / 16;
+  if (s == EC_OK && n16) {
+    const uint8_t* da[EC_MAX_K];
+    uint8_t* oa[EC_MAX_M];
+    for (int j = 0; j < k; ++j) da[j] = d[j] + head;
+    for (int i = 0; i < m; ++i) oa[i] = o[i] + head;
+    s = kRsTable[k - 1][m - 1](coeff, da, oa, n16, st);
+  }
+  const uint64_t done = head + n16 * 16;
+  if (s == EC_OK && done < nbytes) s = launch_generic(coeff, k, m, d, o, done, nbytes - done, st);
   return s;
 }
 
@@ -851,22 +868,28 @@ int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64
   if (!d_data || !d_parity || k < 1) return EC_EINVAL;
   if (k > EC_MAX_K) return EC_ERANGE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  bool aligned = ec::aligned16(d_parity);
-  for (int j = 0; j < k; ++j) {
+  for (int j = 0; j < k; ++j)
     if (!d_data[j]) return EC_EINVAL;
-    aligned &= ec::aligned16(d_data[j]);
-  }
   if (nbytes == 0) return EC_OK;
   uint8_t ones[EC_MAX_K];
   for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
   uint8_t* const out[1] = {d_parity};
-  if (!aligned || k > ec::kFastMaxK)
+  const int skew = ec::common_skew(out, 1, ec::common_skew(d_data, k, -1));
+  if (skew < 0 || k > ec::kFastMaxK)
     return ec::launch_generic(ones, k, 1, d_data, out, 0, nbytes, st);
-  const uint64_t n16 = nbytes / 16;
+  uint64_t head = skew ? 16u - (uint64_t)skew : 0;
+  if (head > nbytes) head = nbytes;
   int s = EC_OK;
-  if (n16) s = ec::kXorTable[k - 1](d_data, d_parity, n16, st);
-  if (s == EC_OK && (nbytes & 15))
-    s = ec::launch_generic(ones, k, 1, d_data, out, n16 * 16, nbytes & 15, st);
+  if (head) s = ec::launch_generic(ones, k, 1, d_data, out, 0, head, st);
+  const uint64_t n16 = (nbytes - head) / 16;
+  if (s == EC_OK && n16) {
+    const uint8_t* da[EC_MAX_K];
+    for (int j = 0; j < k; ++j) da[j] = d_data[j] + head;
+    s = ec::kXorTable[k - 1](da, d_parity + head, n16, st);
+  }
+  const uint64_t done = head + n16 * 16;
+  if (s == EC_OK && done < nbytes)
+    s = ec::launch_generic(ones, k, 1, d_data, out, done, nbytes - done, st);
   return s;
 }
 

@@ -71,6 +71,24 @@ def test_rs_encode_misaligned(pkg, dev, offset):
         assert _eq(p, w)
 
 
+def test_rs_encode_mixed_misalignment(pkg, dev):
+    """Shards misaligned by different amounts (byte path throughout) and by a
+    common amount with the outputs aligned (byte path throughout too)."""
+    rng = np.random.default_rng(31)
+    n = 50_001
+    d = _host(rng, 6, n)
+    dd = [_to_dev([a], dev, off)[0] for a, off in zip(d, [1, 2, 3, 4, 5, 6])]
+    out = [_to_dev([np.zeros(n, np.uint8)], dev, off)[0] for off in (7, 0, 9)]
+    pkg.rs_encode(dd, 3, out=out)
+    want = oracle.rs_encode(oracle.cauchy(6, 3), d)
+    for p, w in zip(out, want):
+        assert _eq(p, w)
+    dd = _to_dev(d, dev, 5)
+    par = pkg.rs_encode(dd, 3)
+    for p, w in zip(par, want):
+        assert _eq(p, w)
+
+
 @pytest.mark.parametrize("k,m", [(20, 6), (32, 16), (17, 1), (5, 9)])
 def test_rs_encode_generic_kernel(pkg, dev, k, m):
     rng = np.random.default_rng(k * m)
@@ -98,10 +116,14 @@ def test_rs_encode_arbitrary_coefficients(pkg, dev):
 @pytest.mark.parametrize("k", list(range(1, 17)) + [20, 32])
 def test_xor_encode(pkg, dev, k):
     rng = np.random.default_rng(100 + k)
-    for n, off in [(4096 * 5 + 48, 0), (777, 0), (9999, 3)]:
+    for n, off in [(4096 * 5 + 48, 0), (777, 0), (9999, 3), (70_000, 11), (5, 13)]:
         d = _host(rng, k, n)
         p = pkg.xor_encode(_to_dev(d, dev, off))
         assert _eq(p, oracle.xor_encode(d)), f"k={k} n={n} off={off}"
+        # output at the same misalignment: head bytes, then the vector path
+        q = _to_dev([np.zeros(n, np.uint8)], dev, off)[0]
+        pkg.xor_encode(_to_dev(d, dev, off), out=q)
+        assert _eq(q, oracle.xor_encode(d)), f"k={k} n={n} off={off} (common skew)"
 
 
 @pytest.mark.parametrize("k,m", [(6, 3), (4, 1), (8, 2)])
