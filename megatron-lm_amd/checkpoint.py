@@ -164,7 +164,7 @@ class GpuSliceCodec:
                 raise CheckpointingException(f"slice {p} has {slices[p].size} bytes, not {S * U}")
         tensors = [torch.empty(tm["shape"], dtype=_dtype(tm["dtype"]), device=device)
                    for tm in meta["tensors"]]
-        lay = self._layout.StripeLayout(tensors, k, m, U)
+        lay = self._layout.StripeLayout(tensors, k, m, U, device=device)
         if lay.n_stripes != S or lay.n_units != meta["n_units"]:
             raise CheckpointingException("checkpoint header does not match its tensors")
         host = torch.empty((k, S, U), dtype=torch.uint8, pin_memory=True)

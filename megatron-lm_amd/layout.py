@@ -32,8 +32,11 @@ def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
     addresses (0 = absent slot of the last stripe) and valid lengths.
     Zero-byte tensors contribute no unit; an empty list gives one empty
     stripe."""
-    base = np.asarray(base, np.uint64)
-    size = np.asarray(size, np.int64)
+    base = np.asarray(base, np.uint64).reshape(-1)
+    size = np.asarray(size, np.int64).reshape(-1)
+    if size.size == 0:
+        empty = np.zeros(0, np.int64)
+        return empty, empty, np.zeros((1, k), np.uint64), np.zeros((1, k), np.uint32)
     n_units = (size + unit_bytes - 1) // unit_bytes
     unit_tensor = np.repeat(np.arange(size.size), n_units)
     first = np.concatenate([[0], np.cumsum(n_units)[:-1]]).astype(np.int64)
@@ -71,7 +74,8 @@ def _hold(stream, *tensors) -> None:
 
 class StripeLayout:
     def __init__(self, tensors: Sequence[torch.Tensor], k: int, m: int,
-                 unit_bytes: int = 64 << 10, coeff: Optional[np.ndarray] = None):
+                 unit_bytes: int = 64 << 10, coeff: Optional[np.ndarray] = None,
+                 device=None):
         if unit_bytes <= 0 or unit_bytes % 16:
             raise ValueError("unit_bytes must be a positive multiple of 16")
         if not (1 <= k <= 16 and 1 <= m <= 4):
@@ -81,9 +85,11 @@ class StripeLayout:
         if self.coeff.shape != (m, k):
             raise ValueError("coefficient matrix must be m x k")
         self.tensors = list(tensors)
-        if not self.tensors:
-            raise ValueError("no tensors")
-        self.device = self.tensors[0].device
+        if self.tensors:
+            self.device = self.tensors[0].device
+        else:  # an empty list codes as one stripe of absent (zero) units
+            self.device = torch.device(device) if device is not None else \
+                torch.device("cuda", torch.cuda.current_device())
         base = np.zeros(len(self.tensors), np.uint64)
         size = np.zeros(len(self.tensors), np.int64)
         for i, t in enumerate(self.tensors):

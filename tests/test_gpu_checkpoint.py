@@ -40,3 +40,15 @@ def test_gpu_checkpoint_recover_three_ranks(tmp_path):
 
 def test_gpu_checkpoint_cleanup_four_ranks(tmp_path):
     launch(tmp_path, "cleanup", world=4, k=2, m=2, unit=1024, use_gpu=True)
+
+
+def test_gpu_empty_tensor_list(pkg, dev):
+    """A rank with nothing to save still takes part: one all-zero stripe."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    pset = pkg.encode([], 4, 2, 256)
+    torch.cuda.synchronize()
+    assert pset.parity.shape == (1, 2, 256) and not pset.parity.any()
+    codec = GpuSliceCodec(4, 2, 256)
+    meta, slices = codec.encode([])
+    assert meta["n_units"] == 0 and all(not s.any() for s in slices)
+    assert codec.decode(meta, {p: slices[p] for p in (1, 2, 4, 5)}, dev) == []

@@ -50,3 +50,19 @@ def test_unit_table_empty(pkg):
     from megatron_lm_amd.layout import unit_table
     owner, idx, P, L = unit_table(np.array([5], np.uint64), np.array([0]), 4, 64)
     assert owner.size == 0 and P.shape == (1, 4) and not P.any() and not L.any()
+
+
+def test_unit_table_empty_list(pkg):
+    from megatron_lm_amd.layout import unit_table
+    owner, idx, P, L = unit_table(np.zeros(0, np.uint64), np.zeros(0, np.int64), 6, 64)
+    assert owner.size == 0 and P.shape == (1, 6) and not P.any() and not L.any()
+
+
+def test_host_tensors_are_rejected_loudly(pkg):
+    """No CPU fallback: host tensors are an error, not a silent slow path."""
+    import torch
+    cpu = [torch.zeros(64, dtype=torch.uint8) for _ in range(4)]
+    for call in (lambda: pkg.xor_encode(cpu), lambda: pkg.rs_encode(cpu, 2),
+                 lambda: pkg.encode(cpu, 4, 2, 64)):
+        with pytest.raises(ValueError, match="device"):
+            call()
