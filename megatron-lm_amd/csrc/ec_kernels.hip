@@ -328,7 +328,12 @@ __global__ void __launch_bounds__(kXorBlock) xor_kernel(const XorArgs<K> a) {
       if (j < K)
         acc = make_uint4(acc.x ^ x[u][j].x, acc.y ^ x[u][j].y, acc.z ^ x[u][j].z,
                          acc.w ^ x[u][j].w);
-      if (idx < a.n16) reinterpret_cast<uint4*>(a.out)[idx] = acc;
+      if (idx < a.n16) {
+        if (K == 1)  // a plain copy: streaming stores measured 3 % faster
+          store_stream(a.out + idx * 16, acc);
+        else
+          reinterpret_cast<uint4*>(a.out)[idx] = acc;
+      }
     }
   }
 }
