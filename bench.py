@@ -1,8 +1,8 @@
 """Benchmark of the erasure-coding hot path on one MI355X.
 
-Headline (BASELINE.json metric): RS(6,3) encode GB/s of data bytes over six
-256 MiB shards of serialized fp32 optimizer state, inputs resident in HBM, and
-its HBM roofline fraction.  Also measured in the same run and reported under
+Headline metric: RS(6,3) encode GB/s of data bytes over six 256 MiB shards of
+serialized fp32 optimizer state, inputs resident in HBM, and its HBM roofline
+fraction.  Also measured in the same run and reported under
 "also": RS(6,3) decode with 3 seeded erasures, XOR parity of 4 x 64 MiB bf16
 shards, the batched configurations, the encode's interference with a GEMM
 load, the checkpoint staging path, and a streaming copy as the practical

@@ -1,4 +1,6 @@
-"""The five BASELINE.json configurations at full size on the GPU.
+"""The five benchmark configurations at full size on the GPU: XOR 4 x 64 MiB,
+RS(6,3) 6 x 256 MiB encode and 3-erasure decode, RS(8,2) over a 20.8 GB rank
+buffer in 4 MiB units, RS(12,4) over 3,000 ragged tensors with a 1% update.
 
 Bit-exact comparisons against the CPU encoder (oracle/ec_cpu_fast.c, itself
 pinned to the scalar oracle by test_oracle.py) where the bytes fit a host
