@@ -43,13 +43,14 @@ namespace {
 constexpr int kBlock = 256;     // lanes per workgroup (4 wavefronts)
 constexpr int kFastMaxK = 16;   // template-instantiated shard counts
 constexpr int kFastMaxM = 4;
-#ifndef EC_SPAN_BYTES
-#define EC_SPAN_BYTES (16u << 10)
-#endif
-// Bytes of each unit a batched workgroup walks (measured on MI355X, HBM
-// traffic: RS(8,2) over 4 MiB units 5.31 TB/s at 64 KiB spans, 5.50 at 32,
-// 5.70 at 16; RS(12,4) over ragged 64 KiB units 5.87 / 5.86 / 6.12).
-constexpr uint32_t kSpanBytes = EC_SPAN_BYTES;
+// Bytes of each unit a batched workgroup walks: 8 KiB for units up to
+// 256 KiB, 16 KiB above.  Measured on MI355X (HBM traffic), spans of
+// 64/32/16/8 KiB: RS(8,2) over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2)
+// over 64 KiB units 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units
+// 5.87/5.86/6.13/6.22.
+inline uint32_t span_bytes(uint32_t unit_bytes) {
+  return unit_bytes <= (256u << 10) ? (8u << 10) : (16u << 10);
+}
 
 // ---------------------------------------------------------------- helpers --
 
@@ -658,6 +659,7 @@ constexpr int unroll_for() {
   return K <= 8 ? 2 : 1;
 }
 
+
 template <int K, int M>
 int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, uint64_t n16,
               hipStream_t st) {
@@ -699,10 +701,10 @@ int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* d
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
   a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
-  // A workgroup walks up to kSpanBytes of each unit, keeping at least 2048
+  // A workgroup walks up to span_bytes() of each unit, keeping at least 2048
   // workgroups (8 per CU) in the launch.
   const uint32_t tile_bytes = kBlock * U * 16u;
-  uint64_t tpb = kSpanBytes / tile_bytes;
+  uint64_t tpb = span_bytes(unit_bytes) / tile_bytes;
   const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
   if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
   if (tpb < 1) tpb = 1;
