@@ -22,9 +22,15 @@ each rank's ordered tensor list:
 * the rank's tensors are cut into stripes of k units of ``unit_bytes``
   (``StripeLayout``) and m parity units are computed on the GPU;
 * codeword position p (data 0..k-1, parity k..k+m-1) of rank r's stripes is
-  a *slice* of n_stripes * unit_bytes bytes held by group rank (r + p) mod G,
-  so the storage of any m ranks can be lost and every rank still decodes
-  (G >= k + m);
+  a *slice* of n_stripes * unit_bytes bytes held by group rank
+  (r + p * jump) mod G, so the storage of any m ranks can be lost and every
+  rank still decodes (the k + m holders must be distinct:
+  G / gcd(jump, G) >= k + m);
+* ``jump`` has the meaning of the reference's ``--replication-jump``
+  (megatron/training/arguments.py:2425-2429: copies of rank n go to n + J,
+  n + 2J, ...).  With ranks numbered node-major and jump = ranks per node,
+  the k + m slices of a rank sit on k + m different nodes, so losing up to m
+  whole nodes still loads;
 * storage is (k + m) / k of the data per rank, and a save moves
   (k + m - 1) / k of it over the network.  Replication with factor F stores
   F times the data and tolerates F - 1 losses.
@@ -218,16 +224,27 @@ class GpuSliceCodec:
 # -------------------------------------------------------------- strategy --
 
 class ErasureCodedStrategy:
-    """(k, m) erasure code over each rank's tensors, slices placed on the
-    next k + m - 1 ranks of the group (see module docstring)."""
+    """(k, m) erasure code over each rank's tensors; slice p of rank r is
+    held by group rank (r + p * jump) mod G (see module docstring)."""
 
     def __init__(self, k: int, m: int, unit_bytes: int = 4 << 20,
-                 group: Optional[dist.ProcessGroup] = None, codec=None):
+                 group: Optional[dist.ProcessGroup] = None, codec=None, jump: int = 1):
         if k < 1 or m < 1:
             raise ValueError("k and m must be positive")
+        if jump < 1:
+            raise ValueError("jump must be positive")
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
-        self.group = group
+        self.group, self.jump = group, jump
         self.codec = codec if codec is not None else GpuSliceCodec(k, m, unit_bytes)
+
+    @classmethod
+    def from_ec_params(cls, k: int, m: int, unit_bytes: int = 4 << 20, jump: int = 1,
+                       group: Optional[dist.ProcessGroup] = None) -> "ErasureCodedStrategy":
+        """Counterpart of the reference's
+        ``CliqueReplicationStrategy.from_replication_params(jump, factor)``
+        (megatron/training/training.py:826-828): the code's shape replaces the
+        replication factor, ``jump`` keeps its meaning."""
+        return cls(k, m, unit_bytes, group=group, jump=jump)
 
     # group helpers
     def ranks(self) -> List[int]:
@@ -237,13 +254,15 @@ class ErasureCodedStrategy:
 
     def holder(self, owner: int, pos: int) -> int:
         r = self.ranks()
-        return r[(r.index(owner) + pos) % len(r)]
+        return r[(r.index(owner) + pos * self.jump) % len(r)]
 
     def check_group(self) -> None:
-        if len(self.ranks()) < self.k + self.m:
+        g = len(self.ranks())
+        # (r + p * jump) mod g takes g / gcd(jump, g) distinct values as p runs.
+        if g // np.gcd(self.jump, g) < self.k + self.m:
             raise CheckpointingException(
-                f"group of {len(self.ranks())} ranks cannot hold k + m = {self.k + self.m} "
-                f"distinct slices")
+                f"group of {g} ranks with jump {self.jump} cannot hold k + m = "
+                f"{self.k + self.m} distinct slices")
 
     def _exchange(self, outgoing: Dict[Tuple[int, int, int], np.ndarray],
                   incoming: List[Tuple[int, int, int, int]]) -> Dict[Tuple[int, int, int], np.ndarray]:

@@ -30,7 +30,7 @@ def same(a, b):
         for x, y in zip(a, b))
 
 
-def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile):
+def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1):
     try:
         sys.path.insert(0, ROOT)
         sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -49,7 +49,7 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile):
         else:
             from ec_cpu_codec import OracleSliceCodec
             codec = OracleSliceCodec(k, m, unit)
-        strat = ErasureCodedStrategy(k, m, unit, codec=codec)
+        strat = ErasureCodedStrategy(k, m, unit, codec=codec, jump=jump)
         mgr = ECLocalCheckpointManager(root, strat)
         mine = make_tensors(rank, device)
         state = TensorListState([t.clone() for t in mine], {"rank": rank})
@@ -58,7 +58,8 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile):
             mgr.save(state, 1)
             dist.barrier()
             names = sorted(f.name for f in mgr.local_dir.iterdir())
-            want = sorted(f"iter_0000001_{(rank - p) % world}_local.ec{p}" for p in range(k + m))
+            want = sorted(f"iter_0000001_{(rank - p * jump) % world}_local.ec{p}"
+                          for p in range(k + m))
             assert names == want, (names, want)
             lost = [(world - 1) - 2 * i for i in range(m)]  # m ranks lose their storage
             if rank in lost:
@@ -69,6 +70,23 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile):
             got, name = mgr.load()
             assert name == f"iter_0000001_{rank}_local", name
             assert same(got.tensors, mine) and got.common == {"rank": rank}
+        elif scenario in ("node_lost", "node_lost_adjacent"):
+            # Two ranks per node, numbered node-major; node 1 (ranks 2, 3) loses
+            # its storage.  With jump = 2 every rank's slices sit on distinct
+            # nodes and the iteration loads; with jump = 1 a rank's slices
+            # share a node and m = 1 cannot cover it.
+            mgr.save(state, 1)
+            dist.barrier()
+            if rank in (2, 3):
+                shutil.rmtree(mgr.local_dir)
+                os.makedirs(mgr.local_dir)
+            dist.barrier()
+            if scenario == "node_lost":
+                assert mgr.find_latest() == 1
+                got, _ = mgr.load()
+                assert same(got.tensors, mine)
+            else:
+                assert mgr.find_latest() == -1
         elif scenario == "cleanup":
             mgr.save(state, 1)
             mgr.save(state, 2)
