@@ -461,7 +461,7 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(enc_traffic_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(k, m, shard),
-                     "kernel": "rs_kernel<6,3,2>",
+                     "kernel": "rs_kernel<6,3,1>",
                      "algorithmic_bytes_per_launch": traffic,
                      "kernel_us": round(ev_ms * 1e3, 2)},
         "cpu_baseline": cpu,

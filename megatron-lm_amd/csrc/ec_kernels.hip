@@ -14,12 +14,14 @@
 //   The m parity outputs of those bytes are accumulated in VGPRs and written
 //   once: every input byte is read from HBM exactly once and every parity
 //   byte written exactly once.  Loads and stores are non-temporal (streamed
-//   past L2 and the Infinity Cache), and tiles are renumbered so that each
-//   of the 8 XCDs walks its own contiguous slice of the shards.  Measured on
+//   past L2 and the Infinity Cache), and tiles are renumbered so that the
+//   shards are streamed at two places at once (split_tile).  Measured on
 //   MI355X for RS(6,3) over 256 MiB shards: plain loads/stores and tables in
 //   SGPRs 5.48 TB/s of HBM traffic; streaming access 5.90; plus LDS tables
-//   6.15; plus the XCD order 6.22 (see gf_matvec16 for the table-read order
-//   that keeps wider codes at the same rate).
+//   6.15; the two-place order with one chunk per lane 6.29-6.54 over five
+//   buffer layouts, where one window per XCD gave 5.69-6.22 (see
+//   gf_matvec16 for the table-read order that keeps wider codes at the same
+//   rate).
 //
 // GF multiply by a coefficient c (see PermTab in gf256.h): the byte x is cut
 // into fields x[2:0], x[5:3], x[7:6]; each field indexes an 8- or 4-entry
@@ -113,14 +115,17 @@ __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
   __builtin_nontemporal_store(w, (global_u32x4*)(uintptr_t)p);
 }
 
-// XCD-aware tile order.  Workgroups are dispatched round-robin over the 8
-// XCDs (workgroup b runs on XCD b % 8); renumbering them so that XCD x gets
-// the contiguous tile range [x*per, (x+1)*per) gives each XCD its own long
-// sequential stream per shard.  A bijection on [0, gridDim.x); the
-// remainder past 8*per keeps its index.
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t nb) {
-  const uint32_t per = nb >> 3;
-  return b < (per << 3) ? (b & 7u) * per + (b >> 3) : b;
+// Two-window tile order.  Workgroups are dispatched round-robin over the 8
+// XCDs (workgroup b runs on XCD b % 8).  Renumbering b -> (b % 2) * per + b / 2
+// gives the even XCDs the first half of the tile range and the odd XCDs the
+// second half, so every shard is streamed at two places half a shard apart.
+// On MI355X this beat launch order (one place) and one window per XCD (eight
+// places) for every code measured, on every buffer layout tried: separate
+// allocations, one packed block, random 4 KiB offsets, 1 MiB and 12 KiB
+// padding.  A bijection on [0, gridDim.x); an odd last tile keeps its index.
+__device__ __forceinline__ uint32_t split_tile(uint32_t b, uint32_t nb) {
+  const uint32_t per = nb >> 1;
+  return b < (per << 1) ? (b & 1u) * per + (b >> 1) : b;
 }
 
 // Copy the m x k permute tables from the kernel arguments into LDS, where
@@ -254,7 +259,7 @@ __global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
   stage_tables<K, M>(tab, a.tab);
   const uint64_t tile = (uint64_t)kBlock * U;
   const uint64_t stride = (uint64_t)gridDim.x * tile;
-  for (uint64_t base = (uint64_t)xcd_tile(blockIdx.x, gridDim.x) * tile + threadIdx.x;
+  for (uint64_t base = (uint64_t)split_tile(blockIdx.x, gridDim.x) * tile + threadIdx.x;
        base < a.n16; base += stride) {
     uint4 x[U][K];
 #pragma unroll
@@ -298,7 +303,8 @@ __device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uin
 
 // XOR parity: 512-lane workgroups in launch order (measured on MI355X for
 // XOR(4) over 64 MiB shards: 6.37 TB/s of HBM traffic; 6.21 with 256 lanes;
-// 5.68 with the XCD tile order, which only pays off for the RS kernels).
+// 5.68 with one tile window per XCD and 6.00 with split_tile's two, which
+// only pay off for the RS kernel).
 constexpr int kXorBlock = 512;
 
 template <int K, int U>
@@ -669,7 +675,9 @@ int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, 
   for (int i = 0; i < M; ++i)
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   a.n16 = n16;
-  constexpr int U = unroll_for<K>();
+  // One 16-byte chunk per lane per shard: with the two-window order this beat
+  // two chunks by 2-6 % for k <= 8 (k > 8 needs U = 1 for registers anyway).
+  constexpr int U = 1;
   hipLaunchKernelGGL((rs_kernel<K, M, U>), dim3(grid_for(n16, U)), dim3(kBlock), 0, st, a);
   return hip_status();
 }
