@@ -617,6 +617,13 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     if (off >= a.unit_bytes) continue;
     const bool fast = aligned && (t + 1) * (kBlock * 16u) <= full;
     uint32_t acc[M][4] = {};
+    // The parity loads do not depend on the delta: issue them first so that
+    // they are in flight together with the unit loads.
+    uint4 pv[M];
+    if (fast) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) pv[i] = load_stream(p[i] + off);
+    }
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       if (nw[j] == nullptr) continue;  // uniform: unchanged unit
@@ -637,7 +644,7 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-      const uint4 v = fast ? load_stream(p[i] + off) : load_unit(p[i], off, a.unit_bytes);
+      const uint4 v = fast ? pv[i] : load_unit(p[i], off, a.unit_bytes);
       const uint4 w = make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]);
       if (fast)
         store_stream(p[i] + off, w);
@@ -739,12 +746,14 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
   a.tiles_per_unit = (unit16 + kBlock - 1) / kBlock;
-  // Spans of up to 64 KiB per unit, keeping at least 16384 workgroups: each
-  // tile is a dependent chain (unit loads, then the parity read-modify-
-  // write), so the update needs more workgroups in flight than the encode.
-  uint64_t tpb = (64u << 10) / (kBlock * 16u);
+  // One tile per workgroup: each tile is a dependent chain (unit and parity
+  // loads, then the parity store), so the update wants as many workgroups
+  // in flight as it has tiles.  Measured for the 1 % update of 3,000 ragged
+  // tensors in 64 KiB units (RS(12,4), 2,993 stripes): 3-tile spans 0.382 ms,
+  // one tile 0.343 ms, one tile with the parity loads issued first 0.338 ms.
+  // Spans grow only to keep the grid near 2^30 workgroups.
   const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
-  if (total_tiles / tpb < 16384) tpb = total_tiles / 16384;
+  uint64_t tpb = (total_tiles + 0x3fffffffull) >> 30;
   if (tpb < 1) tpb = 1;
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
