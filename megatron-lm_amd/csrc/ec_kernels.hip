@@ -46,10 +46,12 @@ constexpr int kBlock = 256;     // lanes per workgroup (4 wavefronts)
 constexpr int kFastMaxK = 16;   // template-instantiated shard counts
 constexpr int kFastMaxM = 4;
 // Bytes of each unit a batched workgroup walks: 8 KiB for units up to
-// 256 KiB, 16 KiB above.  Measured on MI355X (HBM traffic), spans of
-// 64/32/16/8 KiB: RS(8,2) over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2)
-// over 64 KiB units 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units
-// 5.87/5.86/6.13/6.22.
+// 256 KiB, 16 KiB above, and never less than one tile.  Measured on MI355X
+// (HBM traffic, two chunks per lane for k <= 8), spans of 64/32/16/8 KiB:
+// RS(8,2) over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2) over 64 KiB
+// units 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units
+// 5.87/5.86/6.13/6.22.  With four chunks per lane (batched_unroll) a k <= 8
+// tile is 16 KiB, so those codes run one tile per workgroup.
 inline uint32_t span_bytes(uint32_t unit_bytes) {
   return unit_bytes <= (256u << 10) ? (8u << 10) : (16u << 10);
 }
@@ -452,6 +454,7 @@ __device__ __align__(16) uint8_t g_zero_tile[kBlock * 4 * 16] = {0};
 template <int K, int M, int U>
 __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
                                           const PermTab (&tab)[M][K]) {
+  static_assert(kBlock * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
   uint4 x[U][K];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -672,6 +675,18 @@ constexpr int unroll_for() {
   return K <= 8 ? 2 : 1;
 }
 
+// Chunks per lane of the batched launcher.  For k <= 8 a workgroup takes one
+// 16 KiB tile per unit (U = 4, 222 VGPRs for RS(8,2), two waves per SIMD):
+// fewer workgroups in flight means fewer stripes open at once, and this
+// beat U = 2 with 16 KiB spans by 0-4 % (RS(8,2) over the 20.8 GB rank
+// buffer in 4 MiB units 5.73 -> 5.86 TB/s of traffic; 1 MiB units 5.96 ->
+// 6.19; RS(6,3) in 4 MiB units 5.81 -> 5.96; 64 KiB units 6.52 -> 6.67).
+// Wider codes keep U = 1 (RS(12,4) ragged: U = 2 was 3 % slower).
+template <int K>
+constexpr int batched_unroll() {
+  return K <= 8 ? 4 : 1;
+}
+
 
 template <int K, int M>
 int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, uint64_t n16,
@@ -712,12 +727,12 @@ int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* d
   a.olen = olen;
   for (int i = 0; i < M; ++i)
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
-  constexpr int U = unroll_for<K>();
+  constexpr int U = batched_unroll<K>();
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
   a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
-  // A workgroup walks up to span_bytes() of each unit, keeping at least 2048
-  // workgroups (8 per CU) in the launch.
+  // A workgroup walks up to span_bytes() of each unit (at least one tile),
+  // keeping at least 2048 workgroups (8 per CU) in the launch.
   const uint32_t tile_bytes = kBlock * U * 16u;
   uint64_t tpb = span_bytes(unit_bytes) / tile_bytes;
   const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
