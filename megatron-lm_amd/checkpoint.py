@@ -144,16 +144,16 @@ class GpuSliceCodec:
         pptr = self._dev(pptr, np.int64, dev)
         _lib.check(_lib.lib().ec_encode_batched(
             _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
-            pptr.data_ptr(), S, U, stream_handle()), "ec_encode_batched")
+            pptr.data_ptr(), S, U, stream_handle(None, dev)), "ec_encode_batched")
         # gather: every data unit (s, p) to row s of slice p, one k=m=1 launch
         optr = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1), np.int64, dev)
         one = np.ones((1, 1), np.uint8)
         _lib.check(_lib.lib().ec_encode_batched(
             _lib.u8ptr(one), 1, 1, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(), optr.data_ptr(),
-            S * k, U, stream_handle()), "ec_encode_batched (gather)")
+            S * k, U, stream_handle(None, dev)), "ec_encode_batched (gather)")
         host = torch.empty((k + m, S, U), dtype=torch.uint8, pin_memory=True)
         host.copy_(block, non_blocking=True)
-        torch.cuda.current_stream().synchronize()
+        torch.cuda.current_stream(dev).synchronize()
         meta = {"k": k, "m": m, "unit_bytes": U, "n_stripes": S, "n_units": lay.n_units,
                 "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
         return meta, [host[p].numpy().reshape(-1) for p in range(k + m)]
@@ -199,7 +199,7 @@ class GpuSliceCodec:
                     self._dev(optr, np.int64, device), self._dev(olen, np.int32, device)]
             _lib.check(_lib.lib().ec_decode_batched(
                 _lib.u8ptr(one), 1, 1, *[t.data_ptr() for t in args], sptr.size, U,
-                stream_handle()), "ec_decode_batched (scatter)")
+                stream_handle(None, device)), "ec_decode_batched (scatter)")
         # rebuild the missing data positions from the k slices, one launch
         lost_data = [p for p in range(k) if p not in slices or p not in avail]
         if lost_data:
@@ -216,8 +216,8 @@ class GpuSliceCodec:
                     self._dev(lay.host_len[:, lost_data], np.int32, device)]
             _lib.check(_lib.lib().ec_decode_batched(
                 _lib.u8ptr(rows), k, len(lost_data), *[t.data_ptr() for t in args], S, U,
-                stream_handle()), "ec_decode_batched")
-        torch.cuda.current_stream().synchronize()
+                stream_handle(None, device)), "ec_decode_batched")
+        torch.cuda.current_stream(device).synchronize()
         return tensors
 
 

@@ -20,18 +20,32 @@ import torch
 from . import _lib
 
 
-def _dev(t: torch.Tensor, what: str):
+def _dev(t: torch.Tensor, what: str, device: Optional[torch.device] = None):
+    """(address, byte size) of a contiguous device tensor, optionally checked
+    to live on ``device``."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{what} must be a torch.Tensor")
     if not t.is_cuda:
         raise ValueError(f"{what} must be a device (HIP) tensor")
     if not t.is_contiguous():
         raise ValueError(f"{what} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{what} is on {t.device}, the other operands on {device}")
     return t.data_ptr(), t.numel() * t.element_size()
 
 
-def stream_handle(stream: Optional[torch.cuda.Stream] = None) -> ctypes.c_void_p:
-    s = stream if stream is not None else torch.cuda.current_stream()
+def stream_handle(stream: Optional[torch.cuda.Stream] = None,
+                  device: Optional[torch.device] = None) -> ctypes.c_void_p:
+    """The opaque ``ec_stream_t`` of ``stream``, or of the current stream of
+    ``device`` (torch's current device if None).  The kernels run on the
+    stream's device, so a stream on another device than the data is
+    rejected."""
+    if stream is None:
+        s = torch.cuda.current_stream(device)
+    else:
+        s = stream
+        if device is not None and s.device != torch.device(device):
+            raise ValueError(f"stream is on {s.device}, the tensors on {device}")
     return ctypes.c_void_p(s.cuda_stream)
 
 
@@ -81,7 +95,8 @@ def decode_matrix(coeff: np.ndarray, erased: Sequence[int]):
 def _shards(shards: Sequence[torch.Tensor], what: str):
     if len(shards) == 0:
         raise ValueError(f"no {what}")
-    ptrs, sizes = zip(*[_dev(t, f"{what}[{i}]") for i, t in enumerate(shards)])
+    device = shards[0].device if isinstance(shards[0], torch.Tensor) else None
+    ptrs, sizes = zip(*[_dev(t, f"{what}[{i}]", device) for i, t in enumerate(shards)])
     if len(set(sizes)) != 1:
         raise ValueError(f"{what} differ in byte size: {sorted(set(sizes))}")
     return list(ptrs), sizes[0]
@@ -94,7 +109,7 @@ def _outputs(out, n: int, nbytes: int, device, what: str) -> List[torch.Tensor]:
     if len(out) != n:
         raise ValueError(f"{what}: expected {n} tensors, got {len(out)}")
     for i, t in enumerate(out):
-        _, nb = _dev(t, f"{what}[{i}]")
+        _, nb = _dev(t, f"{what}[{i}]", device)
         if nb != nbytes:
             raise ValueError(f"{what}[{i}] has {nb} bytes, shards have {nbytes}")
     return out
@@ -106,7 +121,8 @@ def xor_encode(shards: Sequence[torch.Tensor], out: Optional[torch.Tensor] = Non
     ptrs, nbytes = _shards(shards, "shards")
     (out,) = _outputs(None if out is None else [out], 1, nbytes, shards[0].device, "out")
     _lib.check(_lib.lib().ec_xor_encode(_lib.ptr_array(ptrs), len(ptrs), out.data_ptr(),
-                                        nbytes, stream_handle(stream)), "ec_xor_encode")
+                                        nbytes, stream_handle(stream, shards[0].device)),
+               "ec_xor_encode")
     return out
 
 
@@ -121,7 +137,8 @@ def matvec(coeff: np.ndarray, shards: Sequence[torch.Tensor], out=None, stream=N
     outs = _outputs(out, m, nbytes, shards[0].device, "out")
     fn = _lib.lib().ec_rs_encode if what == "ec_rs_encode" else _lib.lib().ec_rs_decode
     _lib.check(fn(_lib.u8ptr(coeff), k, m, _lib.ptr_array(ptrs),
-                  _lib.ptr_array([t.data_ptr() for t in outs]), nbytes, stream_handle(stream)),
+                  _lib.ptr_array([t.data_ptr() for t in outs]), nbytes,
+                  stream_handle(stream, shards[0].device)),
                what)
     return outs
 

@@ -86,16 +86,14 @@ class StripeLayout:
             raise ValueError("coefficient matrix must be m x k")
         self.tensors = list(tensors)
         if self.tensors:
-            self.device = self.tensors[0].device
+            self.device = getattr(self.tensors[0], "device", None)
         else:  # an empty list codes as one stripe of absent (zero) units
             self.device = torch.device(device) if device is not None else \
                 torch.device("cuda", torch.cuda.current_device())
         base = np.zeros(len(self.tensors), np.uint64)
         size = np.zeros(len(self.tensors), np.int64)
         for i, t in enumerate(self.tensors):
-            if t.device != self.device:
-                raise ValueError("all tensors must be on one device")
-            p, nb = _dev(t, f"tensors[{i}]")
+            p, nb = _dev(t, f"tensors[{i}]", self.device)
             base[i], size[i] = p, nb
         self.tensor_bytes = size
         (self.unit_tensor, self.unit_index, self.host_ptrs,
@@ -130,7 +128,7 @@ class StripeLayout:
         pp = cached[1]
         _lib.check(_lib.lib().ec_encode_batched(
             _lib.u8ptr(self.coeff), self.k, self.m, self.d_ptrs.data_ptr(), self.d_len.data_ptr(),
-            pp.data_ptr(), self.n_stripes, self.unit_bytes, stream_handle(stream)),
+            pp.data_ptr(), self.n_stripes, self.unit_bytes, stream_handle(stream, self.device)),
             "ec_encode_batched")
         _hold(stream, pp)
         return parity
@@ -138,7 +136,7 @@ class StripeLayout:
     def _parity_ptrs_check(self, parity: torch.Tensor) -> None:
         if parity.shape != (self.n_stripes, self.m, self.unit_bytes) or parity.dtype != torch.uint8:
             raise ValueError("parity must be uint8 [n_stripes, m, unit_bytes]")
-        _dev(parity, "parity")
+        _dev(parity, "parity", self.device)
 
     def _to_dev(self, a: np.ndarray, dt) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(a).view(dt).copy()).to(self.device)
@@ -150,13 +148,21 @@ class StripeLayout:
         """Descriptors for rebuilding the units at codeword positions ``lost``
         (data positions 0..k-1 into the tensors, parity positions k..k+m-1
         into ``parity``) of the given stripes (default: all); at most m
-        positions.  None if nothing is lost."""
+        positions.  None if nothing is lost or no stripe is given."""
         lost = sorted(set(int(x) for x in lost))
         if not lost:
             return None
         k, m = self.k, self.m
         surv, rows = decode_matrix(self.coeff, lost)
-        st = np.arange(self.n_stripes) if stripes is None else np.asarray(stripes, np.int64)
+        if stripes is None:
+            st = np.arange(self.n_stripes)
+        else:
+            st = np.asarray(stripes, np.int64).reshape(-1)
+            if st.size and (st.min() < 0 or st.max() >= self.n_stripes or
+                            np.unique(st).size != st.size):
+                raise ValueError(f"stripes must be distinct indices in [0, {self.n_stripes})")
+            if st.size == 0:
+                return None
         self._parity_ptrs_check(parity)
         par_base = np.uint64(parity.data_ptr())
 
@@ -212,7 +218,7 @@ class StripeLayout:
         optr = np.zeros((st.size, k), np.uint64)
         ln = np.zeros((st.size, k), np.uint32)
         for n, (r, j) in enumerate(zip(inv, pos)):
-            p, nb = _dev(old_units[n], f"old_units[{n}]")
+            p, nb = _dev(old_units[n], f"old_units[{n}]", self.device)
             if nb < self.host_len[stripe[n], j]:
                 raise ValueError(f"old_units[{n}] is shorter than the unit")
             nptr[r, j] = self.host_ptrs[stripe[n], j]
@@ -241,12 +247,14 @@ class StripeLayout:
         if plan.kind == "decode":
             st = _lib.lib().ec_decode_batched(
                 _lib.u8ptr(plan.rows), self.k, plan.outputs, a.data_ptr(), b.data_ptr(),
-                c.data_ptr(), d.data_ptr(), plan.n_stripes, self.unit_bytes, stream_handle(stream))
+                c.data_ptr(), d.data_ptr(), plan.n_stripes, self.unit_bytes,
+                stream_handle(stream, self.device))
             _lib.check(st, "ec_decode_batched")
         else:
             st = _lib.lib().ec_parity_update(
                 _lib.u8ptr(plan.rows), self.k, self.m, a.data_ptr(), b.data_ptr(), c.data_ptr(),
-                d.data_ptr(), plan.n_stripes, self.unit_bytes, stream_handle(stream))
+                d.data_ptr(), plan.n_stripes, self.unit_bytes,
+                stream_handle(stream, self.device))
             _lib.check(st, "ec_parity_update")
         _hold(stream, a, b, c, d)
 

@@ -245,10 +245,14 @@ def test_batched_encode_matches_oracle(pkg, dev, k, m, unit, misalign):
     assert np.array_equal(par.cpu().numpy(), _oracle_layout_parity(layout, host, unit))
 
 
-@pytest.mark.parametrize("lost", [(0,), (3, 13), (0, 5, 12, 15), (12, 13, 14, 15), (1, 2, 3, 4)])
-def test_batched_decode_round_trip(pkg, dev, lost):
-    k, m, unit = 12, 4, 4096
-    rng = np.random.default_rng(sum(lost))
+@pytest.mark.parametrize("k,m,unit,lost", [
+    (12, 4, 4096, (0,)), (12, 4, 4096, (3, 13)), (12, 4, 4096, (0, 5, 12, 15)),
+    (12, 4, 4096, (12, 13, 14, 15)), (12, 4, 4096, (1, 2, 3, 4)),
+    # k <= 8 runs four chunks per lane (16 KiB tiles): units shorter and
+    # longer than one tile
+    (8, 2, 4096, (0, 9)), (8, 2, 40960, (3, 7)), (6, 3, 65536, (0, 4, 7)), (5, 1, 1024, (2,))])
+def test_batched_decode_round_trip(pkg, dev, k, m, unit, lost):
+    rng = np.random.default_rng(sum(lost) + 100 * k + unit)
     host, tensors = _ragged_device(rng, dev, 50, 5 * unit, misalign=True)
     pset = pkg.encode(tensors, k, m, unit)
     par_ref = pset.parity.clone()
@@ -267,9 +271,42 @@ def test_batched_decode_round_trip(pkg, dev, lost):
     assert torch.equal(pset.parity, par_ref)
 
 
-def test_batched_update_equals_reencode(pkg, dev):
-    k, m, unit = 12, 4, 2048
-    rng = np.random.default_rng(77)
+def test_batched_decode_stripe_subset(pkg, dev):
+    """Decoding a subset of stripes rebuilds exactly those stripes; stripe
+    indices are checked on the host."""
+    k, m, unit = 8, 2, 8192
+    rng = np.random.default_rng(5)
+    host, tensors = _ragged_device(rng, dev, 30, 6 * unit)
+    pset = pkg.encode(tensors, k, m, unit)
+    lay = pset.layout
+    assert lay.n_stripes >= 4
+    pick = [0, 2, lay.n_stripes - 1]
+    for s in range(lay.n_stripes):
+        u = s * k + 1
+        if u < lay.n_units:
+            lay.unit_view(u).fill_(0xA5)
+    lay.decode(pset.parity, [1], stripes=pick)
+    torch.cuda.synchronize()
+    for s in range(lay.n_stripes):
+        u = s * k + 1
+        if u >= lay.n_units:
+            continue
+        t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+        want = host[t].reshape(-1).view(np.uint8)[i * unit: i * unit + int(lay.host_len[s, 1])]
+        got = lay.unit_view(u).cpu().numpy()
+        if s in pick:
+            assert np.array_equal(got, want), s
+        else:
+            assert (got == 0xA5).all(), s
+    for bad in ([lay.n_stripes], [-1], [0, 0]):
+        with pytest.raises(ValueError):
+            lay.plan_decode(pset.parity, [1], stripes=bad)
+    assert lay.plan_decode(pset.parity, [1], stripes=[]) is None
+
+
+@pytest.mark.parametrize("k,m,unit", [(12, 4, 2048), (6, 3, 20480)])
+def test_batched_update_equals_reencode(pkg, dev, k, m, unit):
+    rng = np.random.default_rng(77 + k)
     host, tensors = _ragged_device(rng, dev, 60, 8 * unit)
     pset = pkg.encode(tensors, k, m, unit)
     lay = pset.layout
