@@ -10,6 +10,8 @@ Modules:
   codec    equal-size shards: xor_encode, rs_encode, reconstruct, host algebra
   layout   ragged tensor lists -> units -> stripes; batched encode/decode/update
   api      the drop-in entry points encode / decode / update
+  checkpoint  ECLocalCheckpointManager + ErasureCodedStrategy (the repl_strategy slot)
+  args     --non-persistent-ckpt-type in_memory: flags, validation, checkpointing context
 """
 from . import _lib
 from ._lib import ECError, ECLibraryMissing, SingularError
