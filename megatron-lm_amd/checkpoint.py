@@ -43,6 +43,7 @@ scatter and reconstruction on load) goes through the engine's C ABI; the
 """
 from __future__ import annotations
 
+import io
 import json
 import os
 import re
@@ -288,23 +289,51 @@ class ErasureCodedStrategy:
         return {key: v.numpy() for key, v in recv.items()}
 
 
-def _pack(header: dict, payload: np.ndarray) -> np.ndarray:
-    h = json.dumps(header, sort_keys=True).encode()
-    out = np.empty(len(_MAGIC) + 8 + len(h) + payload.size, np.uint8)
+def _pack(header: dict, payload: np.ndarray, state: bytes = b"") -> np.ndarray:
+    """Slice file: magic, u64 header length, JSON header (whose
+    ``state_bytes`` gives the length of what follows), the serialized hollow
+    state (empty for a plain tensor list), then the slice bytes."""
+    h = json.dumps({**header, "state_bytes": len(state)}, sort_keys=True).encode()
+    start = len(_MAGIC) + 8
+    out = np.empty(start + len(h) + len(state) + payload.size, np.uint8)
     out[: len(_MAGIC)] = np.frombuffer(_MAGIC, np.uint8)
-    out[len(_MAGIC): len(_MAGIC) + 8] = np.frombuffer(np.uint64(len(h)).tobytes(), np.uint8)
-    out[len(_MAGIC) + 8: len(_MAGIC) + 8 + len(h)] = np.frombuffer(h, np.uint8)
-    out[len(_MAGIC) + 8 + len(h):] = payload
+    out[len(_MAGIC): start] = np.frombuffer(np.uint64(len(h)).tobytes(), np.uint8)
+    out[start: start + len(h)] = np.frombuffer(h, np.uint8)
+    if state:
+        out[start + len(h): start + len(h) + len(state)] = np.frombuffer(state, np.uint8)
+    out[start + len(h) + len(state):] = payload
     return out
 
 
-def _unpack(blob: np.ndarray) -> Tuple[dict, np.ndarray]:
+def _unpack(blob: np.ndarray) -> Tuple[dict, bytes, np.ndarray]:
     if bytes(blob[: len(_MAGIC)]) != _MAGIC:
         raise CheckpointingException("not an erasure-coded checkpoint slice")
-    n = int(np.frombuffer(bytes(blob[len(_MAGIC): len(_MAGIC) + 8]), np.uint64)[0])
     start = len(_MAGIC) + 8
+    n = int(np.frombuffer(bytes(blob[len(_MAGIC): start]), np.uint64)[0])
     header = json.loads(bytes(blob[start: start + n]).decode())
-    return header, blob[start + n:]
+    ns = int(header.get("state_bytes", 0))
+    state = bytes(blob[start + n: start + n + ns])
+    return header, state, blob[start + n + ns:]
+
+
+def _hollow_state(state) -> bytes:
+    """The state without its tensors, serialized, for a state that follows
+    the tensor protocol of MCoreTensorAwareStateDict (pop_tensors /
+    insert_tensors, megatron/core/dist_checkpointing/tensor_aware_state_dict.py:195-232):
+    the tensors are popped, the hollow object is saved with torch.save (as the
+    reference's local manager saves the whole object), and the tensors are
+    put back, so the caller's state is unchanged.  Empty for a plain list or
+    a TensorListState, whose ``common`` dict travels as JSON instead."""
+    if isinstance(state, TensorListState) or not (
+            hasattr(state, "pop_tensors") and hasattr(state, "insert_tensors")):
+        return b""
+    tensors = state.pop_tensors()
+    try:
+        buf = io.BytesIO()
+        torch.save(state, buf)
+        return buf.getvalue()
+    finally:
+        state.insert_tensors(tensors)
 
 
 # --------------------------------------------------------------- manager --
@@ -359,13 +388,15 @@ class ECLocalCheckpointManager:
         error = None
         received: Dict[Tuple[int, int, int], np.ndarray] = {}
         try:
-            tensors = state.tensors if hasattr(state, "tensors") else list(state)
-            common = getattr(state, "common", {})
+            # .tensors of MCoreTensorAwareStateDict is an iterator: take it once
+            tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
+            hollow = _hollow_state(state)
+            common = state.common if isinstance(state, TensorListState) else {}
             meta, slices = st.codec.encode(tensors)
             meta["common"] = common
             meta["owner"] = me
             meta["iteration"] = iteration
-            blobs = {p: _pack({**meta, "pos": p}, s) for p, s in enumerate(slices)}
+            blobs = {p: _pack({**meta, "pos": p}, s, hollow) for p, s in enumerate(slices)}
             sizes = torch.tensor([blobs[p].size for p in range(st.k + st.m)], dtype=torch.int64)
         except Exception as e:  # noqa: BLE001 - reported collectively below
             error = e
@@ -469,9 +500,17 @@ class ECLocalCheckpointManager:
         self.latest_iteration = it
         return it
 
-    def load(self) -> Tuple[TensorListState, str]:
+    def load(self) -> Tuple[object, str]:
         """Read back the newest iteration all ranks can decode, rebuilding this
-        rank's lost slices from any k of its k + m.  Collective."""
+        rank's lost slices from any k of its k + m.  Collective.
+
+        Returns (state, name).  A state saved through the tensor protocol (a
+        MCoreTensorAwareStateDict) comes back as that object, restored from
+        the files this manager wrote (torch.load of the hollow object, as the
+        reference's local manager loads its own files) with the rebuilt
+        tensors inserted, ready for ``to_state_dict``
+        (megatron/training/checkpointing.py:891-899).  Anything else comes
+        back as a TensorListState."""
         self.wait()
         st = self.strategy
         it, plan = self._plan()
@@ -493,18 +532,23 @@ class ECLocalCheckpointManager:
         blobs = dict(local)
         for (src, owner, pos), buf in got.items():
             blobs[pos] = buf
-        slices, meta = {}, None
+        slices, meta, hollow = {}, None, b""
         for pos, blob in blobs.items():
-            header, payload = _unpack(blob)
+            header, state_bytes, payload = _unpack(blob)
             if header.get("owner") != me or header.get("iteration") != it or header.get("pos") != pos:
                 raise CheckpointingException("slice header does not match its name")
             if header.get("generator") != GENERATOR_ID:
                 raise CheckpointingException(f"unknown generator {header.get('generator')!r}")
             meta = header
+            hollow = hollow or state_bytes
             slices[pos] = payload
         device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else torch.device("cpu")
         tensors = st.codec.decode(meta, slices, device)
         self.latest_iteration = it
+        if hollow:
+            state = torch.load(io.BytesIO(hollow), weights_only=False)
+            state.insert_tensors(tensors)
+            return state, self._ckpt_id(it)
         return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
 
 

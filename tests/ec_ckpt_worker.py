@@ -87,6 +87,29 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
                 assert same(got.tensors, mine)
             else:
                 assert mgr.find_latest() == -1
+        elif scenario == "tasd":
+            # A tensor-aware state dict round trip: the object comes back with
+            # its non-tensor part, the rebuilt tensors inserted, after a rank
+            # lost its storage.
+            from ec_tasd_double import FakeTensorAwareStateDict
+            names = [f"t{i}" for i in range(len(mine))]
+            common = {"rank": rank, "iteration": 5, "opt": {"lr": 1e-4, "betas": (0.9, 0.95)}}
+            tasd = FakeTensorAwareStateDict([t.clone() for t in mine], common, names)
+            kept = list(tasd.tensors)
+            mgr.save(tasd, 5)
+            assert not tasd.is_hollow and all(a is b for a, b in zip(tasd.tensors, kept))
+            dist.barrier()
+            if rank == world - 1:
+                shutil.rmtree(mgr.local_dir)
+                os.makedirs(mgr.local_dir)
+            dist.barrier()
+            got, name = mgr.load()
+            assert isinstance(got, FakeTensorAwareStateDict), type(got)
+            assert name == f"iter_0000005_{rank}_local" and not got.is_hollow
+            assert got.common == common and got.names == names
+            assert same(list(got.tensors), mine)
+            sd = got.to_state_dict()
+            assert sd["common"] == common and set(sd) == {"common", *names}
         elif scenario == "cleanup":
             mgr.save(state, 1)
             mgr.save(state, 2)

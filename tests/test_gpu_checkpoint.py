@@ -42,6 +42,11 @@ def test_gpu_checkpoint_cleanup_four_ranks(tmp_path):
     launch(tmp_path, "cleanup", world=4, k=2, m=2, unit=1024, use_gpu=True)
 
 
+def test_gpu_checkpoint_tensor_aware_state_three_ranks(tmp_path):
+    """A tensor-aware state dict comes back as itself, tensors rebuilt on the GPU."""
+    launch(tmp_path, "tasd", world=3, k=2, m=1, unit=2048, use_gpu=True)
+
+
 def test_gpu_empty_tensor_list(pkg, dev):
     """A rank with nothing to save still takes part: one all-zero stripe."""
     from megatron_lm_amd.checkpoint import GpuSliceCodec
