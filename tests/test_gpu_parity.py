@@ -320,3 +320,35 @@ def test_batched_update_equals_reencode(pkg, dev, k, m, unit):
     fresh = lay.encode()
     torch.cuda.synchronize()
     assert torch.equal(pset.parity, fresh)
+
+
+@pytest.mark.parametrize("k", [2, 9])
+def test_batched_largest_unit(pkg, dev, k):
+    """unit_bytes at its 2 GiB maximum (the kernels' 32-bit in-unit offsets
+    end there), with the last unit ending 4103 bytes short of a tile
+    boundary.  Checked by size-independent properties: the batched parity
+    equals the flat kernel's over the zero-padded units (the flat kernel is
+    checked against the oracle above), and a lost unit decodes back."""
+    unit = 1 << 31
+    m = 1
+    n = (k - 1) * unit + unit - 4096 - 7
+    g = torch.Generator(device=dev)
+    g.manual_seed(11 + k)
+    data = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g)
+    pset = pkg.encode([data], k, m, unit)
+    lay = pset.layout
+    assert lay.n_stripes == 1 and int(lay.host_len[0, k - 1]) == unit - 4096 - 7
+    last = torch.zeros(unit, dtype=torch.uint8, device=dev)
+    last[: n - (k - 1) * unit].copy_(data[(k - 1) * unit:])
+    shards = [data[j * unit: (j + 1) * unit] for j in range(k - 1)] + [last]
+    (flat,) = pkg.rs_encode(shards, m, coeff=lay.coeff)
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity[0, 0], flat)
+    del flat, shards
+    for lost in (0, k - 1):
+        keep = lay.unit_view(lost).clone()
+        lay.unit_view(lost).fill_(0xA5)
+        pkg.decode(pset, [lost])
+        torch.cuda.synchronize()
+        assert torch.equal(lay.unit_view(lost), keep), lost
+        del keep
