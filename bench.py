@@ -252,6 +252,44 @@ def overlap_with_training(pkg, dev, data, parity, coeff) -> dict:
             "overlap_encode_GBps_with_gemm": round(data_bytes / e_both / 1e6, 1)}
 
 
+def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
+    """Practical ceiling of the RS(6,3) access pattern on this box: the RS
+    kernel's memory skeleton (libec_probe.so: same loads, stores and tile
+    order, the GF arithmetic replaced by one XOR) over 256 MiB streams, with
+    6 reads only, 3 writes only, and both.  6 reads and 3 writes run back to
+    back would move 9 / (6 / read + 3 / write) bytes per unit time: the bound
+    the encode is compared with."""
+    import ctypes
+    import torch
+    path = os.path.join(os.path.dirname(pkg.library_path()), "libec_probe.so")
+    if not os.path.exists(path):
+        return {}
+    lib = ctypes.CDLL(path)
+    lib.ecp_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                               ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    ins = [torch.empty(shard, dtype=torch.uint8, device=dev).random_(0, 256) for _ in range(6)]
+    outs = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(3)]
+    sink = torch.zeros(16, dtype=torch.uint8, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ptrs = lambda ts: (ctypes.c_void_p * max(1, len(ts)))(*[t.data_ptr() for t in ts])
+
+    def run(r, w):
+        rc = lib.ecp_stream(ptrs(ins[:r]), r, ptrs(outs[:w]), w, shard, sink.data_ptr(), st)
+        if rc:
+            raise RuntimeError(f"ecp_stream({r}, {w}) returned {rc}")
+    out = {}
+    for name, r, w in (("read6", 6, 0), ("write3", 0, 3), ("mix63", 6, 3)):
+        _, ev = timed(lambda: run(r, w), 50, 10)
+        out[name] = (r + w) * shard / (ev * 1e-3) / 1e9
+    bound = 9 / (6 / out["read6"] + 3 / out["write3"])
+    del ins, outs
+    return {"skeleton_read6_GBps": round(out["read6"], 1),
+            "skeleton_write3_GBps": round(out["write3"], 1),
+            "skeleton_mix63_GBps": round(out["mix63"], 1),
+            "mix_bound_GBps": round(bound, 1),
+            "encode_frac_of_mix_bound": round(enc_traffic_gbs / bound, 4)}
+
+
 def ragged_tensors(synth, dev, seed: int):
     """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB)."""
     import torch
@@ -433,6 +471,8 @@ def main() -> int:
     torch_copy_gbs = 2 * src.numel() / (tev * 1e-3) / 1e9
     del src, dst
     log(f"streaming copy {copy_gbs:.0f} GB/s, torch D2D copy {torch_copy_gbs:.0f} GB/s (read+write)")
+    skel = skeleton_ceilings(pkg, dev, shard, enc_traffic_gbs)
+    log(f"memory skeleton: {skel}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -474,6 +514,7 @@ def main() -> int:
             "copy_ceiling_GBps": round(copy_gbs, 1),
             "torch_d2d_copy_GBps": round(torch_copy_gbs, 1),
             "encode_frac_of_copy_ceiling": round(enc_traffic_gbs / copy_gbs, 4),
+            **skel,
         },
     }
     print(json.dumps(result), flush=True)

@@ -1,0 +1,103 @@
+// ec_probe.hip — bandwidth probes that bench.py uses to measure the practical
+// HBM ceiling of the RS kernels' access pattern on the box it runs on.  Not
+// part of the C ABI of ec_mi355.h and not used by the product path.
+//
+// probe_kernel<R, W> is rs_kernel's memory skeleton: 256-lane workgroups, one
+// 16-byte non-temporal load per lane from each of R streams at the same
+// column, the same two-window tile order, and one non-temporal store to each
+// of W streams; the GF(2^8) arithmetic is replaced by one XOR.  With W = 0
+// the XOR result is stored to a 16-byte sink only if all four words equal a
+// value no data hits in practice, which keeps the loads alive; the sink is a
+// valid buffer either way.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxStreams = 8;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+
+__device__ __forceinline__ u32x4 load_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load((const global_u32x4*)(uintptr_t)p);
+}
+__device__ __forceinline__ void store_nt(uint8_t* p, u32x4 v) {
+  __builtin_nontemporal_store(v, (global_u32x4*)(uintptr_t)p);
+}
+
+// Same renumbering as the RS kernel: even XCDs take the first half of the
+// tiles, odd XCDs the second half.
+__device__ __forceinline__ uint32_t split_tile(uint32_t b, uint32_t nb) {
+  const uint32_t per = nb >> 1;
+  return b < (per << 1) ? (b & 1u) * per + (b >> 1) : b;
+}
+
+struct ProbeArgs {
+  const uint8_t* src[kMaxStreams];
+  uint8_t* dst[kMaxStreams];
+  uint8_t* sink;
+  uint64_t n16;
+};
+
+template <int R, int W>
+__global__ void __launch_bounds__(kBlock) probe_kernel(const ProbeArgs a) {
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t idx = (uint64_t)split_tile(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
+       idx < a.n16; idx += stride) {
+    u32x4 acc = {(uint32_t)idx, 0x9e3779b9u, 0x7f4a7c15u, 0x85ebca6bu};
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc ^= load_nt(a.src[j] + idx * 16);
+    if constexpr (W == 0) {
+      if (acc.x == 0xa5a5a5a5u && acc.y == 0xa5a5a5a5u && acc.z == 0xa5a5a5a5u &&
+          acc.w == 0xa5a5a5a5u)
+        store_nt(a.sink, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) store_nt(a.dst[i] + idx * 16, acc);
+    }
+  }
+}
+
+template <int R, int W>
+int launch(const ProbeArgs& a, hipStream_t st) {
+  const uint64_t tiles = (a.n16 + kBlock - 1) / kBlock;
+  const unsigned grid = (unsigned)(tiles < (1u << 20) ? (tiles ? tiles : 1) : (1u << 20));
+  hipLaunchKernelGGL((probe_kernel<R, W>), dim3(grid), dim3(kBlock), 0, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Streams R inputs and W outputs of nbytes each (a multiple of 16, 16-byte
+// aligned pointers) through the skeleton; out[i] = a fixed pattern XOR the
+// inputs.  Supported (R, W): (6, 0), (0, 3), (6, 3), (1, 1).  sink: 16 bytes
+// of device memory.  Returns 0, -1 (bad arguments) or -4 (launch error).
+int ecp_stream(const uint8_t* const* src, int n_src, uint8_t* const* dst, int n_dst,
+               uint64_t nbytes, uint8_t* sink, void* stream) {
+  if (n_src < 0 || n_dst < 0 || n_src > kMaxStreams || n_dst > kMaxStreams || !sink) return -1;
+  if (nbytes % 16 || (reinterpret_cast<uintptr_t>(sink) & 15u)) return -1;
+  ProbeArgs a = {};
+  for (int j = 0; j < n_src; ++j) {
+    if (!src || !src[j] || (reinterpret_cast<uintptr_t>(src[j]) & 15u)) return -1;
+    a.src[j] = src[j];
+  }
+  for (int i = 0; i < n_dst; ++i) {
+    if (!dst || !dst[i] || (reinterpret_cast<uintptr_t>(dst[i]) & 15u)) return -1;
+    a.dst[i] = dst[i];
+  }
+  a.sink = sink;
+  a.n16 = nbytes / 16;
+  if (a.n16 == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n_src == 6 && n_dst == 0) return launch<6, 0>(a, st);
+  if (n_src == 0 && n_dst == 3) return launch<0, 3>(a, st);
+  if (n_src == 6 && n_dst == 3) return launch<6, 3>(a, st);
+  if (n_src == 1 && n_dst == 1) return launch<1, 1>(a, st);
+  return -1;
+}
+
+}  // extern "C"
