@@ -175,19 +175,25 @@ class GpuSliceCodec:
         if lay.n_stripes != S or lay.n_units != meta["n_units"]:
             raise CheckpointingException("checkpoint header does not match its tensors")
         host = torch.empty((k, S, U), dtype=torch.uint8, pin_memory=True)
-        hv = host.numpy()
-        # Copy the slices into the pinned block in parallel pieces (numpy
-        # releases the GIL for large copies): one thread moves ~10 GB/s.
+        block = torch.empty((k, S, U), dtype=torch.uint8, device=device)
+        # Copy the slices into the pinned block in 64 MiB pieces on a thread
+        # pool (numpy releases the GIL for large copies; one thread moves
+        # ~10 GB/s), and start each piece's host-to-device transfer as soon as
+        # the piece is in place, so the copies overlap the transfer.
         pieces = [(r, a, min(a + (64 << 20), S * U)) for r in range(k)
                   for a in range(0, S * U, 64 << 20)]
-        flat = hv.reshape(k, -1)
+        flat = host.numpy().reshape(k, -1)
+        hflat, dflat = host.view(k, -1), block.view(k, -1)
 
         def put(piece):
             r, a, b = piece
             flat[r, a:b] = slices[avail[r]][a:b]
-        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
-            list(pool.map(put, pieces))
-        block = host.to(device, non_blocking=True)
+        with torch.cuda.device(device), \
+                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+            for piece, done in zip(pieces, [pool.submit(put, pc) for pc in pieces]):
+                done.result()
+                r, a, b = piece
+                dflat[r, a:b].copy_(hflat[r, a:b], non_blocking=True)
         one = np.ones((1, 1), np.uint8)
         # scatter the data slices we have into the tensors, one k=m=1 launch
         have = [(r, p) for r, p in enumerate(avail) if p < k]
