@@ -47,11 +47,10 @@ import io
 import json
 import os
 import re
-import threading
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Dict, List, Optional, Sequence, Tuple
+from typing import Callable, Dict, List, NamedTuple, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -354,7 +353,6 @@ class ECLocalCheckpointManager:
         self.strategy = repl_strategy
         self.rank = dist.get_rank()
         self.latest_iteration = -1
-        self._pending: Optional[threading.Thread] = None
 
     # paths
     @property
@@ -383,11 +381,18 @@ class ECLocalCheckpointManager:
         """Encode this rank's tensors, place the k + m slices on their holders
         and write them.  Collective over the strategy's group.  Raises
         CheckpointingException on every rank if any rank fails; then no slice
-        of this iteration is left behind.  With is_async the GPU work and the
-        exchange still run here (no GPU work may move to a writer process);
-        only the file writes go to a thread, and the returned handle's
-        ``wait()`` finishes them."""
-        self.wait()
+        of this iteration is left behind.
+
+        With is_async the GPU work and the exchange still run here (no GPU
+        work may move to a writer process, megatron/core/dist_checkpointing/
+        strategies/async_utils.py:199), and the file writes are returned as an
+        ``AsyncSaveRequest``: the fields and methods of the reference's
+        ``AsyncRequest`` (async_utils.py:37-95), which checkpointing.py:616-645
+        extends with ``add_finalize_fn`` and hands to ``schedule_async_save``.
+        Its ``async_fn`` is a module-level function of picklable arguments, so
+        either async caller (forked or persistent) can run it; its finalize
+        function checks the files and agrees on success across the group.
+        ``execute_sync()`` runs it all in place."""
         st = self.strategy
         st.check_group()
         me = self.rank
@@ -426,30 +431,25 @@ class ECLocalCheckpointManager:
                 if st.holder(me, p) == me:
                     received[(me, p)] = blobs[p]
 
-        def write():
-            ok = True
-            try:
-                self.local_dir.mkdir(parents=True, exist_ok=True)
-                for (owner, p), blob in received.items():
-                    path = self._slice_path(iteration, owner, p)
-                    tmp = path.with_name(path.name + ".tmp")
-                    with open(tmp, "wb") as f:
-                        f.write(blob.tobytes())
-                    os.replace(tmp, path)
-            except Exception:  # noqa: BLE001
-                ok = False
-            return ok
-
         if failed:
             raise CheckpointingException(
                 f"erasure-coded save of iteration {iteration} failed on some rank") from error
+        jobs = [(str(self._slice_path(iteration, owner, p)), torch.from_numpy(blob))
+                for (owner, p), blob in sorted(received.items())]
+        expected = [(path, int(t.numel())) for path, t in jobs]
+
+        def finalize():
+            ok = all(os.path.isfile(path) and os.path.getsize(path) == n for path, n in expected)
+            self._finish_save(iteration, ok)
+
+        self.local_dir.mkdir(parents=True, exist_ok=True)
         if is_async:
-            handle = _AsyncSave(self, iteration, write)
-            self._pending = handle
-            handle.start()
-            return handle
-        ok = write()
-        self._finish_save(iteration, ok)
+            return AsyncSaveRequest(_write_slice_files, (jobs,), [finalize])
+        try:
+            _write_slice_files(jobs)
+        except OSError:
+            pass  # finalize() sees the missing files and fails the save everywhere
+        finalize()
         return None
 
     def _finish_save(self, iteration: int, ok: bool) -> None:
@@ -468,11 +468,6 @@ class ECLocalCheckpointManager:
             mt = _NAME_RE.match(f.name)
             if mt and pred(int(mt.group(1))):
                 f.unlink()
-
-    def wait(self) -> None:
-        if self._pending is not None:
-            h, self._pending = self._pending, None
-            h.wait()
 
     # find / load
     def _plan(self) -> Tuple[int, Dict[int, List[Tuple[int, int, int]]]]:
@@ -501,7 +496,6 @@ class ECLocalCheckpointManager:
         return -1, {}
 
     def find_latest(self) -> int:
-        self.wait()
         it, _ = self._plan()
         self.latest_iteration = it
         return it
@@ -517,7 +511,6 @@ class ECLocalCheckpointManager:
         tensors inserted, ready for ``to_state_dict``
         (megatron/training/checkpointing.py:891-899).  Anything else comes
         back as a TensorListState."""
-        self.wait()
         st = self.strategy
         it, plan = self._plan()
         if it < 0:
@@ -558,25 +551,47 @@ class ECLocalCheckpointManager:
         return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
 
 
-class _AsyncSave:
-    """Handle of an asynchronous save: file writes on a thread; ``wait()``
-    joins it and runs the collective success check."""
+def _write_slice_files(jobs: Sequence[Tuple[str, torch.Tensor]]) -> None:
+    """``async_fn`` of an asynchronous save: write each (path, uint8 CPU
+    tensor) pair atomically (tmp + rename).  No GPU work; module-level with
+    picklable arguments, so it can run in a forked or a spawned writer."""
+    for path, data in jobs:
+        tmp = path + ".tmp"
+        with open(tmp, "wb") as f:
+            f.write(memoryview(data.numpy()))
+        os.replace(tmp, path)
 
-    def __init__(self, mgr: ECLocalCheckpointManager, iteration: int, write):
-        self.mgr, self.iteration, self.write = mgr, iteration, write
-        self.ok = False
-        self.thread = threading.Thread(target=self._run, daemon=True)
-        self.done = False
 
-    def _run(self):
-        self.ok = self.write()
+class AsyncSaveRequest(NamedTuple):
+    """The reference's ``AsyncRequest``
+    (megatron/core/dist_checkpointing/strategies/async_utils.py:37-95) field
+    for field, so that its async queue schedules it unchanged (it checks the
+    field count, freezes the request, and ships it without the finalize
+    functions to the writer, :510-519).  ``async_fn(*async_fn_args)`` writes
+    the files; the finalize functions run afterwards on every rank."""
+    async_fn: Optional[Callable]
+    async_fn_args: Tuple
+    finalize_fns: List[Callable]
+    async_fn_kwargs: Dict = {}
+    preload_fn: Optional[Callable] = None
+    is_frozen: bool = False
+    call_idx: int = 0
 
-    def start(self):
-        self.thread.start()
+    def add_finalize_fn(self, fn: Callable) -> None:
+        if self.is_frozen:
+            raise RuntimeError("Cannot add finalization functions to a frozen AsyncRequest")
+        self.finalize_fns.append(fn)
 
-    def wait(self):
-        if self.done:
-            return
-        self.thread.join()
-        self.done = True
-        self.mgr._finish_save(self.iteration, self.ok)
+    def execute_sync(self) -> None:
+        """Write, synchronise the ranks, then finalize, in the caller."""
+        if self.async_fn is not None:
+            try:
+                self.async_fn(*self.async_fn_args, **self.async_fn_kwargs)
+            except OSError:
+                pass  # the finalize function sees the missing files
+        dist.barrier()
+        for fn in self.finalize_fns:
+            fn()
+
+    def freeze(self) -> "AsyncSaveRequest":
+        return self._replace(is_frozen=True)

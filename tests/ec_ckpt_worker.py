@@ -110,6 +110,23 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             assert same(list(got.tensors), mine)
             sd = got.to_state_dict()
             assert sd["common"] == common and set(sd) == {"common", *names}
+        elif scenario == "async_write_lost":
+            # one rank's writer never ran: finalize fails on every rank and
+            # leaves nothing of that iteration, the previous one stays
+            mgr.save(state, 1)
+            req = mgr.save(state, 2, is_async=True)
+            if rank != 1:
+                req.async_fn(*req.async_fn_args)
+            dist.barrier()
+            try:
+                for fn in req.finalize_fns:
+                    fn()
+                raise AssertionError("finalize of an unwritten save did not raise")
+            except CheckpointingException:
+                pass
+            names = {f.name for f in mgr.local_dir.iterdir()}
+            assert not any(n.startswith("iter_0000002") for n in names), names
+            assert mgr.find_latest() == 1
         elif scenario == "cleanup":
             mgr.save(state, 1)
             mgr.save(state, 2)
@@ -142,10 +159,42 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             except CheckpointingException:
                 pass
         elif scenario == "async":
-            h = mgr.save(state, 3, is_async=True)
-            h.wait()
-            got, _ = mgr.load()
-            assert same(got.tensors, mine)
+            # What the reference's async queue does with the request
+            # (megatron/core/dist_checkpointing/strategies/async_utils.py:498-519,
+            # :172-206): add finalize functions, freeze, ship it without them
+            # to a forked writer (or pickled to a spawned one), then finalize
+            # on every rank.
+            import pickle
+            req = mgr.save(state, 3, is_async=True)
+            assert len(req._fields) == 7 and req.async_fn is not None and req.preload_fn is None
+            done = []
+            req.add_finalize_fn(lambda: done.append(3))
+            frozen = req.freeze()
+            try:
+                frozen.add_finalize_fn(lambda: None)
+                raise AssertionError("a frozen request accepted a finalize function")
+            except RuntimeError:
+                pass
+            ship = frozen._replace(call_idx=1, finalize_fns=[])
+            pickle.dumps(ship)
+            proc = torch.multiprocessing.get_context("fork").Process(
+                target=ship.async_fn, args=ship.async_fn_args, kwargs=ship.async_fn_kwargs)
+            proc.start()
+            proc.join()
+            assert proc.exitcode == 0
+            dist.barrier()
+            for fn in frozen.finalize_fns:
+                fn()
+            assert done == [3] and mgr.latest_iteration == 3
+            got, name = mgr.load()
+            assert name == f"iter_0000003_{rank}_local" and same(got.tensors, mine)
+            # execute_sync: the same request run in place
+            req = mgr.save(state, 4, is_async=True)
+            req.execute_sync()
+            names = {f.name for f in mgr.local_dir.iterdir()}
+            assert not any(n.startswith("iter_0000003") for n in names), names
+            got, name = mgr.load()
+            assert name == f"iter_0000004_{rank}_local" and same(got.tensors, mine)
         else:
             raise ValueError(scenario)
         dist.barrier()
