@@ -35,11 +35,14 @@ each rank's ordered tensor list:
   (k + m - 1) / k of it over the network.  Replication with factor F stores
   F times the data and tolerates F - 1 losses.
 
-Slices are exchanged over the group's ``torch.distributed`` backend with CPU
-tensors (send/recv), and files are written as a JSON header plus raw bytes:
-nothing is pickled.  The GPU work (encode, gather of units into slices,
-scatter and reconstruction on load) goes through the engine's C ABI; the
-``codec`` argument exists so the exchange can be tested without a GPU.
+Slices and inventories are exchanged over the group's ``torch.distributed``
+backend as CPU tensors (send/recv, all_gather), and files are written as a
+JSON header plus raw bytes.  The one serialized object is the hollow state of
+a ``MCoreTensorAwareStateDict`` (its non-tensor part, torch.save), stored
+with the slices so that ``load`` returns the object it was given, as the
+reference's local manager does.  The GPU work (encode, gather of units into
+slices, scatter and reconstruction on load) goes through the engine's C ABI;
+the ``codec`` argument exists so the exchange can be tested without a GPU.
 """
 from __future__ import annotations
 
@@ -376,6 +379,24 @@ class ECLocalCheckpointManager:
                         (int(mt.group(2)), int(mt.group(3)), f.stat().st_size))
         return inv
 
+    def _gather_inventories(self) -> List[np.ndarray]:
+        """Every rank's inventory as int64 rows (iteration, owner, pos,
+        nbytes), exchanged as tensors (no pickled objects): the row counts
+        first, then the rows padded to the longest list."""
+        st = self.strategy
+        rows = np.array([(it, o, p, n) for it, entries in sorted(self._inventory().items())
+                         for o, p, n in sorted(entries)], np.int64).reshape(-1, 4)
+        g = len(st.ranks())
+        count = torch.tensor([rows.shape[0]], dtype=torch.int64)
+        counts = [torch.empty_like(count) for _ in range(g)]
+        dist.all_gather(counts, count, group=st.group)
+        width = max(1, max(int(c[0]) for c in counts))
+        mine = torch.zeros((width, 4), dtype=torch.int64)
+        mine[: rows.shape[0]] = torch.from_numpy(rows)
+        every = [torch.empty_like(mine) for _ in range(g)]
+        dist.all_gather(every, mine, group=st.group)
+        return [e[: int(c[0])].numpy() for e, c in zip(every, counts)]
+
     # save
     def save(self, state, iteration: int, is_async: bool = False):
         """Encode this rank's tensors, place the k + m slices on their holders
@@ -474,16 +495,14 @@ class ECLocalCheckpointManager:
         """Agree on the newest iteration every owner can decode, and for each
         owner the k slices to read: {owner: [(holder, pos, nbytes)]}."""
         st = self.strategy
-        inv = self._inventory()
-        gathered: List[dict] = [None] * len(st.ranks())
-        dist.all_gather_object(gathered, inv, group=st.group)
+        gathered = self._gather_inventories()
         by_iter: Dict[int, Dict[int, Dict[int, Tuple[int, int]]]] = {}
-        for holder, hinv in zip(st.ranks(), gathered):
-            for it, entries in hinv.items():
-                for owner, pos, n in entries:
-                    if st.holder(owner, pos) != holder:
-                        continue  # stray file
-                    by_iter.setdefault(it, {}).setdefault(owner, {})[pos] = (holder, n)
+        members = set(st.ranks())
+        for holder, rows in zip(st.ranks(), gathered):
+            for it, owner, pos, n in rows.tolist():
+                if owner not in members or pos >= st.k + st.m or st.holder(owner, pos) != holder:
+                    continue  # stray file (another group, code or placement)
+                by_iter.setdefault(it, {}).setdefault(owner, {})[pos] = (holder, n)
         for it in sorted(by_iter, reverse=True):
             owners = by_iter[it]
             if all(len(owners.get(o, {})) >= st.k for o in st.ranks()):
