@@ -127,6 +127,16 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             names = {f.name for f in mgr.local_dir.iterdir()}
             assert not any(n.startswith("iter_0000002") for n in names), names
             assert mgr.find_latest() == 1
+        elif scenario == "stray":
+            # files of another group or another code in the directory are ignored
+            mgr.save(state, 1)
+            (mgr.local_dir / "iter_0000009_99_local.ec0").write_bytes(b"x" * 10)
+            (mgr.local_dir / f"iter_0000009_{rank}_local.ec40").write_bytes(b"y" * 10)
+            (mgr.local_dir / "notes.txt").write_bytes(b"z")
+            dist.barrier()
+            assert mgr.find_latest() == 1
+            got, _ = mgr.load()
+            assert same(got.tensors, mine)
         elif scenario == "cleanup":
             mgr.save(state, 1)
             mgr.save(state, 2)
