@@ -105,7 +105,9 @@ int ec_decode_matrix(const uint8_t* coeff, int k, int m, const int* erased,
  * of k device pointers.  Any alignment: when all pointers (inputs and
  * output) share one misalignment modulo 16, the bytes past the first 16-byte
  * boundary take the vector path; otherwise the byte path does all of it.
- * The same holds for ec_rs_encode and ec_rs_decode.  Serves manager.save at
+ * The same holds for ec_rs_encode and ec_rs_decode.  nbytes = 0 returns
+ * EC_OK without touching the shard pointers (empty tensors may have null
+ * addresses); so do those two.  Serves manager.save at
  * checkpointing.py:538-541 for m = 1. */
 int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity,
                   uint64_t nbytes, ec_stream_t stream);

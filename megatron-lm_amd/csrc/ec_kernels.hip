@@ -857,11 +857,11 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
   if (!coeff || !d || !o) return EC_EINVAL;
   if (k < 1 || m < 1) return EC_EINVAL;
   if (k > EC_MAX_K || m > EC_MAX_M) return EC_ERANGE;
+  if (nbytes == 0) return EC_OK;  // empty shards may have null addresses
   for (int j = 0; j < k; ++j)
     if (!d[j]) return EC_EINVAL;
   for (int i = 0; i < m; ++i)
     if (!o[i]) return EC_EINVAL;
-  if (nbytes == 0) return EC_OK;
   // Shards misaligned by the same amount (equal-offset views) run the first
   // bytes up to the next 16-byte boundary through the byte kernel and the
   // rest through the vector kernel; different misalignments take the byte
@@ -904,12 +904,13 @@ extern "C" {
 
 int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64_t nbytes,
                   ec_stream_t stream) {
-  if (!d_data || !d_parity || k < 1) return EC_EINVAL;
+  if (!d_data || k < 1) return EC_EINVAL;
   if (k > EC_MAX_K) return EC_ERANGE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (nbytes == 0) return EC_OK;  // empty shards may have null addresses
+  if (!d_parity) return EC_EINVAL;
   for (int j = 0; j < k; ++j)
     if (!d_data[j]) return EC_EINVAL;
-  if (nbytes == 0) return EC_OK;
   uint8_t ones[EC_MAX_K];
   for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
   uint8_t* const out[1] = {d_parity};

@@ -95,6 +95,11 @@ def test_device_entry_points_reject_bad_arguments(pkg):
     assert L.ec_rs_encode(c, 33, 3, nulls, nulls, 16, None) == pkg._lib.EC_ERANGE
     assert L.ec_rs_encode(c, 6, 3, nulls, nulls, 16, None) == pkg._lib.EC_EINVAL
     assert L.ec_xor_encode(nulls, 4, None, 16, None) == pkg._lib.EC_EINVAL
+    # zero bytes: a no-op that succeeds even with the null addresses of empty tensors
+    assert L.ec_rs_encode(c, 6, 3, nulls, nulls, 0, None) == pkg._lib.EC_OK
+    assert L.ec_rs_decode(c, 6, 3, nulls, nulls, 0, None) == pkg._lib.EC_OK
+    assert L.ec_xor_encode(nulls, 4, None, 0, None) == pkg._lib.EC_OK
+    assert L.ec_rs_encode(c, 0, 3, nulls, nulls, 0, None) == pkg._lib.EC_EINVAL
     assert L.ec_rs_decode(c, 6, 17, nulls, nulls, 16, None) == pkg._lib.EC_ERANGE
     one = ctypes.c_void_p(16)
     assert L.ec_encode_batched(c, 6, 3, one, one, one, 1, 100, None) == pkg._lib.EC_EALIGN

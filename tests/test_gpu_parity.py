@@ -352,3 +352,25 @@ def test_batched_largest_unit(pkg, dev, k):
         torch.cuda.synchronize()
         assert torch.equal(lay.unit_view(lost), keep), lost
         del keep
+
+
+def test_zero_byte_inputs(pkg, dev):
+    """Empty shards are a no-op that succeeds; zero-length tensors in a ragged
+    list own no unit and the rest codes as without them."""
+    empty = [torch.empty(0, dtype=torch.uint8, device=dev) for _ in range(6)]
+    par = pkg.rs_encode(empty, 3)
+    assert all(p.numel() == 0 for p in par)
+    assert pkg.xor_encode(empty[:4]).numel() == 0
+    rec = pkg.reconstruct([None, None] + empty[2:] + [par[0], None, par[2]], 6, 3)
+    torch.cuda.synchronize()
+    assert sorted(rec) == [0, 1, 7] and all(t.numel() == 0 for t in rec.values())
+    rng = np.random.default_rng(3)
+    host = [rng.integers(0, 256, n, dtype=np.uint8) for n in (5000, 0, 70000, 0, 1, 0)]
+    tensors = [torch.from_numpy(h).to(dev) for h in host]
+    unit = 4096
+    a = pkg.encode(tensors, 4, 2, unit)
+    b = pkg.encode([t for t in tensors if t.numel()], 4, 2, unit)
+    torch.cuda.synchronize()
+    assert a.layout.n_units == b.layout.n_units and torch.equal(a.parity, b.parity)
+    assert np.array_equal(a.parity.cpu().numpy(),
+                          _oracle_layout_parity(a.layout, host, unit))
