@@ -383,6 +383,63 @@ __global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
   }
 }
 
+// ------------------------------------------------------------ wide kernel --
+// Codes past the instantiated fast path (k > 16 or m > 4, up to 32 x 16) on
+// 16-byte-aligned shards: rs_kernel's column layout and tile order with the
+// m outputs in registers (M is a template parameter) and k read at run time
+// in groups of kWideGroup loads in flight.  The m x k tables do not fit the
+// kernel arguments (10 KiB for 16 x 32), so each workgroup builds them in LDS
+// from the coefficient bytes; the grid is capped at kWideMaxBlocks
+// workgroups, a few per CU, which keeps that build small next to the
+// streaming.
+constexpr int kWideGroup = 8;
+constexpr unsigned kWideMaxBlocks = 8192;
+
+struct WideArgs {
+  const uint8_t* data[EC_MAX_K];
+  uint8_t* out[EC_MAX_M];
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];  // row-major m x k
+  uint64_t n16;
+  int k;
+};
+
+template <int M>
+__global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
+  __shared__ PermTab tab[M * EC_MAX_K];
+  const int k = a.k;
+  for (int t = threadIdx.x; t < M * k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
+  __syncthreads();
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t idx = (uint64_t)split_tile(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
+       idx < a.n16; idx += stride) {
+    uint32_t acc[M][4] = {};
+    for (int j0 = 0; j0 < k; j0 += kWideGroup) {
+      uint4 x[kWideGroup];
+#pragma unroll
+      for (int g = 0; g < kWideGroup; ++g)
+        x[g] = j0 + g < k ? load_stream(a.data[j0 + g] + idx * 16) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int g = 0; g < kWideGroup; ++g) {
+        if (j0 + g >= k) break;
+        Fields f[4];
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x[g], dd));
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+          // Read each table right before its uses (see gf_matvec16).
+          asm volatile("" ::: "memory");
+          const PermTab t = tab[i * k + j0 + g];
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+  }
+}
+
 // ------------------------------------------------ batched stripe kernels --
 // Grid = n_stripes x tiles_per_unit workgroups, stripe-major, so consecutive
 // workgroups stream adjacent bytes of the same k units.  The descriptor of a
@@ -704,6 +761,21 @@ int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, 
   return hip_status();
 }
 
+template <int M>
+int launch_wide(const uint8_t* coeff, int k, const uint8_t* const* d, uint8_t* const* o,
+                uint64_t n16, hipStream_t st) {
+  WideArgs a;
+  for (int j = 0; j < k; ++j) a.data[j] = d[j];
+  for (int i = 0; i < M; ++i) a.out[i] = o[i];
+  for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
+  a.n16 = n16;
+  a.k = k;
+  const uint64_t tiles = (n16 + kBlock - 1) / kBlock;
+  const unsigned grid = (unsigned)(tiles < kWideMaxBlocks ? (tiles ? tiles : 1) : kWideMaxBlocks);
+  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
 template <int K>
 int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st) {
   XorArgs<K> a;
@@ -819,11 +891,18 @@ template <int... Ks>
 constexpr auto xor_table(std::integer_sequence<int, Ks...>) {
   return std::array<XorFn, sizeof...(Ks)>{&launch_xor<Ks + 1>...};
 }
+using WideFn = int (*)(const uint8_t*, int, const uint8_t* const*, uint8_t* const*, uint64_t,
+                       hipStream_t);
+template <int... Ms>
+constexpr auto wide_table(std::integer_sequence<int, Ms...>) {
+  return std::array<WideFn, sizeof...(Ms)>{&launch_wide<Ms + 1>...};
+}
 
 const auto kRsTable = rs_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kBatchTable = batch_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kUpdTable = upd_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kXorTable = xor_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kWideTable = wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
 
 int launch_generic(const uint8_t* coeff, int k, int m, const uint8_t* const* d,
                    uint8_t* const* o, uint64_t offset, uint64_t n, hipStream_t st) {
@@ -867,8 +946,7 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
   // rest through the vector kernel; different misalignments take the byte
   // kernel throughout.
   const int skew = common_skew(o, m, common_skew(d, k, -1));
-  if (skew < 0 || k > kFastMaxK || m > kFastMaxM)
-    return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
+  if (skew < 0) return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
   uint64_t head = skew ? 16u - (uint64_t)skew : 0;
   if (head > nbytes) head = nbytes;
   int s = EC_OK;
@@ -879,7 +957,10 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
     uint8_t* oa[EC_MAX_M];
     for (int j = 0; j < k; ++j) da[j] = d[j] + head;
     for (int i = 0; i < m; ++i) oa[i] = o[i] + head;
-    s = kRsTable[k - 1][m - 1](coeff, da, oa, n16, st);
+    if (k <= kFastMaxK && m <= kFastMaxM)
+      s = kRsTable[k - 1][m - 1](coeff, da, oa, n16, st);
+    else
+      s = kWideTable[m - 1](coeff, k, da, oa, n16, st);
   }
   const uint64_t done = head + n16 * 16;
   if (s == EC_OK && done < nbytes) s = launch_generic(coeff, k, m, d, o, done, nbytes - done, st);
@@ -915,8 +996,7 @@ int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64
   for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
   uint8_t* const out[1] = {d_parity};
   const int skew = ec::common_skew(out, 1, ec::common_skew(d_data, k, -1));
-  if (skew < 0 || k > ec::kFastMaxK)
-    return ec::launch_generic(ones, k, 1, d_data, out, 0, nbytes, st);
+  if (skew < 0) return ec::launch_generic(ones, k, 1, d_data, out, 0, nbytes, st);
   uint64_t head = skew ? 16u - (uint64_t)skew : 0;
   if (head > nbytes) head = nbytes;
   int s = EC_OK;
@@ -925,7 +1005,9 @@ int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64
   if (s == EC_OK && n16) {
     const uint8_t* da[EC_MAX_K];
     for (int j = 0; j < k; ++j) da[j] = d_data[j] + head;
-    s = ec::kXorTable[k - 1](da, d_parity + head, n16, st);
+    uint8_t* const oa[1] = {d_parity + head};
+    s = k <= ec::kFastMaxK ? ec::kXorTable[k - 1](da, d_parity + head, n16, st)
+                           : ec::kWideTable[0](ones, k, da, oa, n16, st);
   }
   const uint64_t done = head + n16 * 16;
   if (s == EC_OK && done < nbytes)

@@ -89,12 +89,28 @@ def test_rs_encode_mixed_misalignment(pkg, dev):
         assert _eq(p, w)
 
 
-@pytest.mark.parametrize("k,m", [(20, 6), (32, 16), (17, 1), (5, 9)])
-def test_rs_encode_generic_kernel(pkg, dev, k, m):
-    rng = np.random.default_rng(k * m)
-    n = 12345
+@pytest.mark.parametrize("k,m", [(20, 6), (32, 16), (17, 1), (5, 9), (16, 5), (32, 1), (9, 16)])
+@pytest.mark.parametrize("offset", [0, 3])
+def test_rs_encode_wide_codes(pkg, dev, k, m, offset):
+    """Codes past the instantiated fast path (k > 16 or m > 4): the wide
+    kernel on aligned shards; with a common misalignment, byte-path head
+    and tail around it."""
+    rng = np.random.default_rng(k * m + offset)
+    n = 12345 + 4096 * 70
     d = _host(rng, k, n)
-    par = pkg.rs_encode(_to_dev(d, dev), m)
+    out = _to_dev([np.zeros(n, np.uint8)] * m, dev, offset)
+    pkg.rs_encode(_to_dev(d, dev, offset), m, out=out)
+    for p, w in zip(out, oracle.rs_encode(oracle.cauchy(k, m), d)):
+        assert _eq(p, w)
+
+
+def test_rs_encode_generic_kernel_mixed_misalignment(pkg, dev):
+    """Different misalignments take the byte path throughout, wide codes too."""
+    k, m, n = 20, 6, 9999
+    rng = np.random.default_rng(5)
+    d = _host(rng, k, n)
+    dd = [_to_dev([a], dev, j % 7)[0] for j, a in enumerate(d)]
+    par = pkg.rs_encode(dd, m)
     for p, w in zip(par, oracle.rs_encode(oracle.cauchy(k, m), d)):
         assert _eq(p, w)
 
