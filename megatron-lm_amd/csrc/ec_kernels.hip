@@ -389,11 +389,12 @@ __global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
 // m outputs in registers (M is a template parameter) and k read at run time
 // in groups of kWideGroup loads in flight.  The m x k tables do not fit the
 // kernel arguments (10 KiB for 16 x 32), so each workgroup builds them in LDS
-// from the coefficient bytes; the grid is capped at kWideMaxBlocks
-// workgroups, a few per CU, which keeps that build small next to the
-// streaming.
+// from the coefficient bytes.  Measured over 256 MiB shards (HBM TB/s): a
+// full grid beat grids capped at 4k-32k workgroups (RS(6,8) 5.34 vs
+// 4.5-5.2, RS(24,4) 5.37 vs 4.7-4.9), so the table build costs less than the
+// lost parallelism; groups of 16 loads halved the rate, groups of 4 were
+// 0-15 % slower than 8.
 constexpr int kWideGroup = 8;
-constexpr unsigned kWideMaxBlocks = 8192;
 
 struct WideArgs {
   const uint8_t* data[EC_MAX_K];
@@ -770,9 +771,7 @@ int launch_wide(const uint8_t* coeff, int k, const uint8_t* const* d, uint8_t* c
   for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
   a.n16 = n16;
   a.k = k;
-  const uint64_t tiles = (n16 + kBlock - 1) / kBlock;
-  const unsigned grid = (unsigned)(tiles < kWideMaxBlocks ? (tiles ? tiles : 1) : kWideMaxBlocks);
-  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid), dim3(kBlock), 0, st, a);
+  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid_for(n16, 1)), dim3(kBlock), 0, st, a);
   return hip_status();
 }
 
