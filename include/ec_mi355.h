@@ -102,10 +102,11 @@ int ec_decode_matrix(const uint8_t* coeff, int k, int m, const int* erased,
 /* ---- device kernels --------------------------------------------------- */
 
 /* XOR parity: d_parity[b] = XOR_{j<k} d_data[j][b].  d_data is a host array
- * of k device pointers.  Any alignment: when all pointers (inputs and
- * output) share one misalignment modulo 16, the bytes past the first 16-byte
- * boundary take the vector path; otherwise the byte path does all of it.
- * The same holds for ec_rs_encode and ec_rs_decode.  nbytes = 0 returns
+ * of k device pointers.  Any alignment: the bytes from the outputs' first
+ * 16-byte boundary on take a vector path when all outputs share one
+ * misalignment modulo 16 (inputs realigned as needed); outputs at different
+ * misalignments take the byte path throughout.  The same holds for
+ * ec_rs_encode and ec_rs_decode.  nbytes = 0 returns
  * EC_OK without touching the shard pointers (empty tensors may have null
  * addresses); so do those two.  Serves manager.save at
  * checkpointing.py:538-541 for m = 1. */

@@ -396,6 +396,36 @@ __global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
 // 0-15 % slower than 8.
 constexpr int kWideGroup = 8;
 
+// 16 bytes at base + off, where off is a multiple of 16 and base may have any
+// alignment r = base mod 16 (uniform: it depends on the shard only).  r = 0
+// is one dwordx4 load; otherwise the two aligned dwordx4 that hold the bytes
+// are loaded and v_alignbyte_b32 ({hi, lo} >> 8 * (byte count)) shifts them
+// into place.  Both aligned
+// blocks hold at least one byte of [base + off, base + off + 16), so no
+// load leaves the 16-byte blocks (and pages) that the shard itself touches.
+template <int Q>
+__device__ __forceinline__ uint4 align_words(const uint4& lo, const uint4& hi, uint32_t sh) {
+  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  return make_uint4(__builtin_amdgcn_alignbyte(w[Q + 1], w[Q], sh),
+                    __builtin_amdgcn_alignbyte(w[Q + 2], w[Q + 1], sh),
+                    __builtin_amdgcn_alignbyte(w[Q + 3], w[Q + 2], sh),
+                    __builtin_amdgcn_alignbyte(w[Q + 4], w[Q + 3], sh));
+}
+
+__device__ __forceinline__ uint4 load_realign(const uint8_t* base, uint64_t off) {
+  const uint32_t r = (uint32_t)reinterpret_cast<uintptr_t>(base) & 15u;
+  if (r == 0) return load_stream(base + off);
+  const uint8_t* b = base - r + off;
+  const uint4 lo = load_stream(b), hi = load_stream(b + 16);
+  const uint32_t sh = r & 3u;
+  switch (r >> 2) {
+    case 0: return align_words<0>(lo, hi, sh);
+    case 1: return align_words<1>(lo, hi, sh);
+    case 2: return align_words<2>(lo, hi, sh);
+    default: return align_words<3>(lo, hi, sh);
+  }
+}
+
 struct WideArgs {
   const uint8_t* data[EC_MAX_K];
   uint8_t* out[EC_MAX_M];
@@ -418,7 +448,7 @@ __global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
       uint4 x[kWideGroup];
 #pragma unroll
       for (int g = 0; g < kWideGroup; ++g)
-        x[g] = j0 + g < k ? load_stream(a.data[j0 + g] + idx * 16) : make_uint4(0, 0, 0, 0);
+        x[g] = j0 + g < k ? load_realign(a.data[j0 + g], idx * 16) : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int g = 0; g < kWideGroup; ++g) {
         if (j0 + g >= k) break;
@@ -940,12 +970,15 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
     if (!d[j]) return EC_EINVAL;
   for (int i = 0; i < m; ++i)
     if (!o[i]) return EC_EINVAL;
-  // Shards misaligned by the same amount (equal-offset views) run the first
-  // bytes up to the next 16-byte boundary through the byte kernel and the
-  // rest through the vector kernel; different misalignments take the byte
-  // kernel throughout.
-  const int skew = common_skew(o, m, common_skew(d, k, -1));
+  // The outputs fix the frame: the bytes up to their next 16-byte boundary
+  // run through the byte kernel, the 16-byte columns after it through a
+  // vector kernel (the fast one when every input shares the outputs'
+  // misalignment, else the wide one, which realigns each input), and the
+  // last partial column through the byte kernel.  Outputs of different
+  // misalignments take the byte kernel throughout.
+  const int skew = common_skew(o, m, -1);
   if (skew < 0) return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
+  const bool same = common_skew(d, k, skew) == skew;
   uint64_t head = skew ? 16u - (uint64_t)skew : 0;
   if (head > nbytes) head = nbytes;
   int s = EC_OK;
@@ -956,7 +989,7 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
     uint8_t* oa[EC_MAX_M];
     for (int j = 0; j < k; ++j) da[j] = d[j] + head;
     for (int i = 0; i < m; ++i) oa[i] = o[i] + head;
-    if (k <= kFastMaxK && m <= kFastMaxM)
+    if (same && k <= kFastMaxK && m <= kFastMaxM)
       s = kRsTable[k - 1][m - 1](coeff, da, oa, n16, st);
     else
       s = kWideTable[m - 1](coeff, k, da, oa, n16, st);
@@ -994,8 +1027,8 @@ int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64
   uint8_t ones[EC_MAX_K];
   for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
   uint8_t* const out[1] = {d_parity};
-  const int skew = ec::common_skew(out, 1, ec::common_skew(d_data, k, -1));
-  if (skew < 0) return ec::launch_generic(ones, k, 1, d_data, out, 0, nbytes, st);
+  const int skew = ec::common_skew(out, 1, -1);
+  const bool same = ec::common_skew(d_data, k, skew) == skew;
   uint64_t head = skew ? 16u - (uint64_t)skew : 0;
   if (head > nbytes) head = nbytes;
   int s = EC_OK;
@@ -1005,8 +1038,8 @@ int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64
     const uint8_t* da[EC_MAX_K];
     for (int j = 0; j < k; ++j) da[j] = d_data[j] + head;
     uint8_t* const oa[1] = {d_parity + head};
-    s = k <= ec::kFastMaxK ? ec::kXorTable[k - 1](da, d_parity + head, n16, st)
-                           : ec::kWideTable[0](ones, k, da, oa, n16, st);
+    s = same && k <= ec::kFastMaxK ? ec::kXorTable[k - 1](da, d_parity + head, n16, st)
+                                   : ec::kWideTable[0](ones, k, da, oa, n16, st);
   }
   const uint64_t done = head + n16 * 16;
   if (s == EC_OK && done < nbytes)

@@ -390,3 +390,37 @@ def test_zero_byte_inputs(pkg, dev):
     assert a.layout.n_units == b.layout.n_units and torch.equal(a.parity, b.parity)
     assert np.array_equal(a.parity.cpu().numpy(),
                           _oracle_layout_parity(a.layout, host, unit))
+
+
+@pytest.mark.parametrize("n", [5, 31, 4096 + 7, 100_003])
+@pytest.mark.parametrize("k,m", [(6, 3), (4, 1), (20, 6)])
+def test_rs_encode_realigned_inputs(pkg, dev, k, m, n):
+    """Inputs at every misalignment 0..15 with aligned outputs: the wide
+    kernel's realigning loads (two aligned loads + v_alignbyte per shard)."""
+    rng = np.random.default_rng(n + 31 * k)
+    d = _host(rng, k, n)
+    dd = [_to_dev([a], dev, j % 16)[0] for j, a in enumerate(d)]
+    par = pkg.rs_encode(dd, m)
+    for p, w in zip(par, oracle.rs_encode(oracle.cauchy(k, m), d)):
+        assert _eq(p, w)
+    x = pkg.xor_encode(dd)
+    assert _eq(x, oracle.xor_encode(d))
+
+
+@pytest.mark.parametrize("n", [1_000_001, 65_537])
+def test_flat_buffer_cut_into_odd_shards(pkg, dev, n):
+    """k shards cut from one flat buffer at multiples of an odd size (each at
+    a different misalignment), encoded and then rebuilt after 3 losses."""
+    k, m = 6, 3
+    rng = np.random.default_rng(n)
+    flat_h = rng.integers(0, 256, k * n, dtype=np.uint8)
+    flat = torch.from_numpy(flat_h).to(dev)
+    shards = [flat[j * n: (j + 1) * n] for j in range(k)]
+    par = pkg.rs_encode(shards, m)
+    d = [flat_h[j * n: (j + 1) * n] for j in range(k)]
+    for p, w in zip(par, oracle.rs_encode(oracle.cauchy(k, m), d)):
+        assert _eq(p, w)
+    rec = pkg.reconstruct([None, shards[1], None, shards[3], shards[4], shards[5],
+                           par[0], None, par[2]], k, m)
+    assert _eq(rec[0], d[0]) and _eq(rec[2], d[2]) and _eq(rec[7], oracle.rs_encode(
+        oracle.cauchy(k, m), d)[1])
