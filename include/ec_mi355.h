@@ -137,7 +137,9 @@ int ec_rs_decode(const uint8_t* rows, int k, int e,
  * 2 GiB (EC_ERANGE).  Units and
  * parity units at 16-byte-aligned addresses take the vector path; others are
  * read and written byte by byte, and no byte past a unit's valid length is
- * read.  k <= 16 and m <= 4 (EC_ERANGE otherwise).  The units come from the ragged
+ * read.  Units of 4 KiB and up stream at HBM rate; smaller units work but
+ * run a slower byte-granular path.  k <= 16 and m <= 4 (EC_ERANGE
+ * otherwise).  The units come from the ragged
  * shard list of tensor_aware_state_dict.py:179-184 (MCoreTensorAwareStateDict
  * .tensors), chunked in order. */
 int ec_encode_batched(const uint8_t* coeff, int k, int m,
