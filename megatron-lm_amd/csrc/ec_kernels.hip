@@ -50,8 +50,9 @@ constexpr int kFastMaxM = 4;
 // (HBM traffic, two chunks per lane for k <= 8), spans of 64/32/16/8 KiB:
 // RS(8,2) over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2) over 64 KiB
 // units 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units
-// 5.87/5.86/6.13/6.22.  With four chunks per lane (batched_unroll) a k <= 8
-// tile is 16 KiB, so those codes run one tile per workgroup.
+// 5.87/5.86/6.13/6.22.  With four chunks per lane (batched_unroll, units
+// that are a multiple of 16 KiB) a k <= 8 tile is 16 KiB, so those codes run
+// one tile per workgroup.
 inline uint32_t span_bytes(uint32_t unit_bytes) {
   return unit_bytes <= (256u << 10) ? (8u << 10) : (16u << 10);
 }
@@ -396,6 +397,15 @@ __global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
 // 0-15 % slower than 8.
 constexpr int kWideGroup = 8;
 
+// Coefficients per step of the wide kernel's inner loop: pairs for m >= 8,
+// where the GF arithmetic bounds the kernel (RS(32,16) 2.49 -> 2.68 TB/s,
+// RS(10,12) 4.03 -> 4.22), single ones below, where the pair form's longer
+// dependency chains cost 2-6 % (RS(24,4) 5.13 vs 4.90).
+template <int M>
+constexpr int kWidePair() {
+  return M >= 8 ? 2 : 1;
+}
+
 // 16 bytes at base + off, where off is a multiple of 16 and base may have any
 // alignment r = base mod 16 (uniform: it depends on the shard only).  r = 0
 // is one dwordx4 load; otherwise the two aligned dwordx4 that hold the bytes
@@ -450,18 +460,38 @@ __global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
       for (int g = 0; g < kWideGroup; ++g)
         x[g] = j0 + g < k ? load_realign(a.data[j0 + g], idx * 16) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int g = 0; g < kWideGroup; ++g) {
+      for (int g = 0; g < kWideGroup; g += kWidePair<M>()) {
         if (j0 + g >= k) break;
-        Fields f[4];
+        if constexpr (kWidePair<M>() == 2) {
+          // Two coefficients per step (three XOR3 instead of two XOR3 and
+          // two XOR).  x[g + 1] is zero past k and a zero byte's products
+          // are zero, so the pair form is exact for an odd k as well.
+          Fields fa[4], fb[4];
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x[g], dd));
+          for (int dd = 0; dd < 4; ++dd) {
+            fa[dd] = fields(word(x[g], dd));
+            fb[dd] = fields(word(x[g + 1], dd));
+          }
+          const int jb = j0 + g + 1 < k ? j0 + g + 1 : j0 + g;
 #pragma unroll
-        for (int i = 0; i < M; ++i) {
-          // Read each table right before its uses (see gf_matvec16).
-          asm volatile("" ::: "memory");
-          const PermTab t = tab[i * k + j0 + g];
+          for (int i = 0; i < M; ++i) {
+            // Read each table right before its uses (see gf_matvec16).
+            asm volatile("" ::: "memory");
+            const PermTab ta = tab[i * k + j0 + g], tb = tab[i * k + jb];
 #pragma unroll
-          for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+            for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac2(acc[i][dd], ta, fa[dd], tb, fb[dd]);
+          }
+        } else {
+          Fields f[4];
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x[g], dd));
+#pragma unroll
+          for (int i = 0; i < M; ++i) {
+            asm volatile("" ::: "memory");
+            const PermTab t = tab[i * k + j0 + g];
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+          }
         }
       }
     }
