@@ -138,8 +138,9 @@ int ec_rs_decode(const uint8_t* rows, int k, int e,
  * parity units at 16-byte-aligned addresses take the vector path; others are
  * read and written byte by byte, and no byte past a unit's valid length is
  * read.  Units of 4 KiB and up stream at HBM rate; smaller units work but
- * run a slower byte-granular path.  k <= 16 and m <= 4 (EC_ERANGE
- * otherwise).  The units come from the ragged
+ * run a slower byte-granular path.  k <= EC_MAX_K and m <= EC_MAX_M
+ * (EC_ERANGE otherwise); k <= 16, m <= 4 run fully unrolled kernels, wider
+ * codes a kernel with k at run time.  The units come from the ragged
  * shard list of tensor_aware_state_dict.py:179-184 (MCoreTensorAwareStateDict
  * .tensors), chunked in order. */
 int ec_encode_batched(const uint8_t* coeff, int k, int m,
@@ -160,7 +161,7 @@ int ec_encode_batched(const uint8_t* coeff, int k, int m,
  *                                               so a tensor's tail unit is
  *                                               restored in place without
  *                                               writing past its end)
- * Same alignment rules and limits as ec_encode_batched (e <= 4).  Serves
+ * Same alignment rules and limits as ec_encode_batched (e <= EC_MAX_M).  Serves
  * manager.load at checkpointing.py:891-894 for ragged shard lists. */
 int ec_decode_batched(const uint8_t* rows, int k, int e,
                       const uint64_t* d_surv_ptrs, const uint32_t* d_surv_len,

@@ -31,9 +31,10 @@ import argparse
 
 IN_MEMORY = "in_memory"
 
-# The engine's batched launcher instantiates k <= 16, m <= 4.
-MAX_DATA_UNITS = 16
-MAX_PARITY_UNITS = 4
+# The engine's batched launcher takes k <= 32, m <= 16 (k <= 16, m <= 4 on
+# its instantiated fast path).
+MAX_DATA_UNITS = 32
+MAX_PARITY_UNITS = 16
 
 
 def _has(parser: argparse.ArgumentParser, flag: str) -> bool:

@@ -775,6 +775,166 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
   }
 }
 
+// --------------------------------------- batched kernels for wide codes --
+// The batched encode/decode and the parity update for codes past the
+// instantiated fast path (k > 16 or m > 4): k at run time, M a template
+// parameter, one 16-byte chunk per lane (4 KiB tiles).  A workgroup stages
+// its stripe's descriptors and the m x k tables in LDS; fast tiles issue the
+// unit loads in groups of kWideGroup, edge tiles take the units one at a
+// time with byte-granular ends, as in the fixed-size kernels.
+constexpr uint32_t kWideTile = kBlock * 16u;
+
+struct BatchWideArgs {
+  const uint64_t* dptr;  // [n_stripes][k] (update: new units, 0 = unchanged)
+  const uint32_t* dlen;  // [n_stripes][k]
+  const uint64_t* optr;  // update: [n_stripes][k] old units; otherwise unused
+  const uint64_t* pptr;  // [n_stripes][m]
+  const uint32_t* olen;  // [n_stripes][m] valid output bytes, or null = whole units
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];  // row-major m x k
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;
+  uint32_t tiles_per_block;
+  uint32_t blocks_per_unit;
+  int k;
+};
+
+template <int M>
+struct WideStripe {
+  PermTab tab[M * EC_MAX_K];
+  const uint8_t* d[EC_MAX_K];
+  const uint8_t* o[EC_MAX_K];
+  uint32_t len[EC_MAX_K];
+  uint8_t* p[M];
+  uint32_t plen[M];
+};
+
+// Tables and stripe s's descriptors into LDS.  Returns, after a barrier,
+// whether any unit or output address is not 16-byte aligned (uniform).
+template <int M>
+__device__ __forceinline__ bool stage_wide(WideStripe<M>& w, const BatchWideArgs& a, uint32_t s,
+                                           bool update) {
+  const int k = a.k;
+  const uint32_t t = threadIdx.x;
+  for (uint32_t i = t; i < (uint32_t)(M * k); i += kBlock) w.tab[i] = dev_perm_tab(a.coeff[i]);
+  if (t < (uint32_t)k) {
+    const uint8_t* d = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * k + t]);
+    const uint32_t l = d ? a.dlen[(uint64_t)s * k + t] : 0u;
+    const uint8_t* o = update && d ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * k + t])
+                                   : nullptr;
+    w.d[t] = d;
+    w.o[t] = o;
+    w.len[t] = l < a.unit_bytes ? l : a.unit_bytes;
+  } else if (t >= 64 && t < 64 + M) {
+    const uint32_t i = t - 64;
+    uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    const uint32_t l = p ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
+    w.p[i] = p;
+    w.plen[i] = l < a.unit_bytes ? l : a.unit_bytes;
+  }
+  __syncthreads();
+  uintptr_t bits = 0;
+  for (int j = 0; j < k; ++j)
+    bits |= reinterpret_cast<uintptr_t>(w.d[j]) | reinterpret_cast<uintptr_t>(w.o[j]);
+#pragma unroll
+  for (int i = 0; i < M; ++i) bits |= reinterpret_cast<uintptr_t>(w.p[i]);
+  return (bits & 15u) != 0;
+}
+
+template <int M>
+__device__ __forceinline__ void wide_mac(uint32_t (&acc)[M][4], const uint4& x,
+                                         const PermTab* col, int k) {
+  Fields f[4];
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x, dd));
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    asm volatile("" ::: "memory");
+    const PermTab t = col[i * k];
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+  }
+}
+
+template <int M>
+__global__ void __launch_bounds__(kBlock) batched_wide_kernel(const BatchWideArgs a) {
+  __shared__ WideStripe<M> w;
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  const bool misaligned = stage_wide<M>(w, a, s, false);
+  const int k = a.k;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t lo = t * kWideTile, hi = lo + kWideTile;
+    const uint32_t off = lo + threadIdx.x * 16u;
+    bool edge = misaligned;
+    for (int j = 0; j < k; ++j) edge |= w.len[j] > lo && w.len[j] < hi;
+#pragma unroll
+    for (int i = 0; i < M; ++i) edge |= w.plen[i] < hi;
+    uint32_t acc[M][4] = {};
+    if (!edge) {
+      for (int j0 = 0; j0 < k; j0 += kWideGroup) {
+        uint4 x[kWideGroup];
+#pragma unroll
+        for (int g = 0; g < kWideGroup; ++g) {
+          const int j = j0 + g;
+          x[g] = j < k && w.len[j] >= hi ? load_stream(w.d[j] + off) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < kWideGroup; ++g) {
+          if (j0 + g >= k) break;
+          wide_mac<M>(acc, x[g], &w.tab[j0 + g], k);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        store_stream(w.p[i] + off, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    } else {
+      if (off >= a.unit_bytes) continue;
+#pragma unroll 1
+      for (int j = 0; j < k; ++j) {
+        if (off >= w.len[j]) continue;
+        wide_mac<M>(acc, load_unit(w.d[j], off, w.len[j]), &w.tab[j], k);
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        if (off < w.plen[i])
+          store_unit_len(w.p[i], off, w.plen[i],
+                         make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  }
+}
+
+// parity[s][i] ^= C[i][j] * (new[s][j] ^ old[s][j]) for the changed units.
+template <int M>
+__global__ void __launch_bounds__(kBlock) update_wide_kernel(const BatchWideArgs a) {
+  __shared__ WideStripe<M> w;
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  stage_wide<M>(w, a, s, true);
+  const int k = a.k;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t off = t * kWideTile + threadIdx.x * 16u;
+    if (off >= a.unit_bytes) continue;
+    uint32_t acc[M][4] = {};
+    uint4 pv[M];  // the parity does not depend on the delta: load it first
+#pragma unroll
+    for (int i = 0; i < M; ++i) pv[i] = load_unit(w.p[i], off, a.unit_bytes);
+#pragma unroll 1
+    for (int j = 0; j < k; ++j) {
+      if (w.d[j] == nullptr || off >= w.len[j]) continue;  // unchanged unit, or past its end
+      const uint4 vn = load_unit(w.d[j], off, w.len[j]);
+      const uint4 vo = load_unit(w.o[j], off, w.len[j]);
+      wide_mac<M>(acc, make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w),
+                  &w.tab[j], k);
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      store_unit(w.p[i], off, make_uint4(pv[i].x ^ acc[i][0], pv[i].y ^ acc[i][1],
+                                         pv[i].z ^ acc[i][2], pv[i].w ^ acc[i][3]));
+  }
+}
+
 // ---------------------------------------------------------- host launch --
 
 inline int hip_status() { return hipGetLastError() == hipSuccess ? EC_OK : EC_EHIP; }
@@ -923,6 +1083,45 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
   return hip_status();
 }
 
+// Wide codes through the batched kernels: encode / decode (update = false,
+// optr unused) or the parity update.  The same span rules as the fixed-size
+// launchers: spans of span_bytes() with at least 2048 workgroups for the
+// encode, one tile per workgroup for the update.
+template <int M>
+int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
+                        const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
+                        uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st) {
+  BatchWideArgs a;
+  a.dptr = dptr;
+  a.dlen = dlen;
+  a.optr = optr;
+  a.pptr = pptr;
+  a.olen = olen;
+  for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
+  a.k = k;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit_bytes / 16u + kBlock - 1) / kBlock;
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  uint64_t tpb = 1;
+  if (!update) {
+    tpb = span_bytes(unit_bytes) / kWideTile;
+    if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
+  } else {
+    tpb = (total_tiles + 0x3fffffffull) >> 30;
+  }
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  if (update)
+    hipLaunchKernelGGL((update_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((batched_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
 // Dispatch tables over the instantiated (K, M) grid.
 using RsFn = int (*)(const uint8_t*, const uint8_t* const*, uint8_t* const*, uint64_t,
                      hipStream_t);
@@ -975,6 +1174,16 @@ const auto kBatchTable = batch_table(std::make_integer_sequence<int, kFastMaxK>{
 const auto kUpdTable = upd_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kXorTable = xor_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kWideTable = wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
+using BatchWideFn = int (*)(const uint8_t*, int, const uint64_t*, const uint32_t*,
+                            const uint64_t*, const uint64_t*, const uint32_t*, uint32_t, uint32_t,
+                            bool, hipStream_t);
+template <int... Ms>
+constexpr auto batch_wide_table(std::integer_sequence<int, Ms...>) {
+  return std::array<BatchWideFn, sizeof...(Ms)>{&launch_batched_wide<Ms + 1>...};
+}
+const auto kBatchWideTable = batch_wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
+
+inline bool fast_shape(int k, int m) { return k <= kFastMaxK && m <= kFastMaxM; }
 
 int launch_generic(const uint8_t* coeff, int k, int m, const uint8_t* const* d,
                    uint8_t* const* o, uint64_t offset, uint64_t n, hipStream_t st) {
@@ -1045,7 +1254,7 @@ int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t*
 int check_batch(const uint8_t* coeff, int k, int m, const void* a, const void* b,
                 const void* c, uint32_t unit_bytes) {
   if (!coeff || !a || !b || !c || k < 1 || m < 1) return EC_EINVAL;
-  if (k > kFastMaxK || m > kFastMaxM) return EC_ERANGE;
+  if (k > EC_MAX_K || m > EC_MAX_M) return EC_ERANGE;
   if (unit_bytes == 0 || (unit_bytes & 15u)) return EC_EALIGN;
   // Byte offsets inside a unit are 32-bit in the kernels, with one tile of
   // headroom past the unit's end.
@@ -1106,9 +1315,12 @@ int ec_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* d_data
   int s = ec::check_batch(coeff, k, m, d_data_ptrs, d_data_len, d_parity_ptrs, unit_bytes);
   if (s != EC_OK) return s;
   if (n_stripes == 0) return EC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!ec::fast_shape(k, m))
+    return ec::kBatchWideTable[m - 1](coeff, k, d_data_ptrs, d_data_len, nullptr, d_parity_ptrs,
+                                      nullptr, n_stripes, unit_bytes, false, st);
   return ec::kBatchTable[k - 1][m - 1](coeff, d_data_ptrs, d_data_len, d_parity_ptrs, nullptr,
-                                       n_stripes, unit_bytes,
-                                       reinterpret_cast<hipStream_t>(stream));
+                                       n_stripes, unit_bytes, st);
 }
 
 int ec_decode_batched(const uint8_t* rows, int k, int e, const uint64_t* d_surv_ptrs,
@@ -1119,9 +1331,12 @@ int ec_decode_batched(const uint8_t* rows, int k, int e, const uint64_t* d_surv_
   if (s != EC_OK) return s;
   if (!d_out_len) return EC_EINVAL;
   if (n_stripes == 0) return EC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!ec::fast_shape(k, e))
+    return ec::kBatchWideTable[e - 1](rows, k, d_surv_ptrs, d_surv_len, nullptr, d_out_ptrs,
+                                      d_out_len, n_stripes, unit_bytes, false, st);
   return ec::kBatchTable[k - 1][e - 1](rows, d_surv_ptrs, d_surv_len, d_out_ptrs, d_out_len,
-                                       n_stripes, unit_bytes,
-                                       reinterpret_cast<hipStream_t>(stream));
+                                       n_stripes, unit_bytes, st);
 }
 
 int ec_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* d_new_ptrs,
@@ -1132,8 +1347,12 @@ int ec_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* d_new_p
   if (s != EC_OK) return s;
   if (!d_len) return EC_EINVAL;
   if (n_stripes == 0) return EC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!ec::fast_shape(k, m))
+    return ec::kBatchWideTable[m - 1](coeff, k, d_new_ptrs, d_len, d_old_ptrs, d_parity_ptrs,
+                                      nullptr, n_stripes, unit_bytes, true, st);
   return ec::kUpdTable[k - 1][m - 1](coeff, d_new_ptrs, d_old_ptrs, d_len, d_parity_ptrs,
-                                     n_stripes, unit_bytes, reinterpret_cast<hipStream_t>(stream));
+                                     n_stripes, unit_bytes, st);
 }
 
 }  // extern "C"

@@ -78,8 +78,8 @@ class StripeLayout:
                  device=None):
         if unit_bytes <= 0 or unit_bytes % 16:
             raise ValueError("unit_bytes must be a positive multiple of 16")
-        if not (1 <= k <= 16 and 1 <= m <= 4):
-            raise ValueError("batched stripes support 1 <= k <= 16 and 1 <= m <= 4")
+        if not (1 <= k <= 32 and 1 <= m <= 16):
+            raise ValueError("batched stripes support 1 <= k <= 32 and 1 <= m <= 16")
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.coeff = cauchy_matrix(k, m) if coeff is None else np.ascontiguousarray(coeff, np.uint8)
         if self.coeff.shape != (m, k):

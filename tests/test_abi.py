@@ -103,7 +103,8 @@ def test_device_entry_points_reject_bad_arguments(pkg):
     assert L.ec_rs_decode(c, 6, 17, nulls, nulls, 16, None) == pkg._lib.EC_ERANGE
     one = ctypes.c_void_p(16)
     assert L.ec_encode_batched(c, 6, 3, one, one, one, 1, 100, None) == pkg._lib.EC_EALIGN
-    assert L.ec_encode_batched(c, 17, 3, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
+    assert L.ec_encode_batched(c, 33, 3, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
+    assert L.ec_encode_batched(c, 6, 17, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
     assert L.ec_decode_batched(c, 6, 3, one, one, one, None, 1, 64, None) == pkg._lib.EC_EINVAL
     assert L.ec_parity_update(c, 6, 3, one, one, None, one, 1, 64, None) == pkg._lib.EC_EINVAL
 

@@ -48,7 +48,8 @@ def test_reference_flags_not_duplicated():
     ([], "without specifying"),
     (["--non-persistent-local-ckpt-dir", "/x", "--replication", "--replication-jump", "2"],
      "--replication"),
-    (["--non-persistent-local-ckpt-dir", "/x", "--ec-data-units", "17"], "--ec-data-units"),
+    (["--non-persistent-local-ckpt-dir", "/x", "--ec-data-units", "33"], "--ec-data-units"),
+    (["--non-persistent-local-ckpt-dir", "/x", "--ec-parity-units", "17"], "--ec-parity-units"),
     (["--non-persistent-local-ckpt-dir", "/x", "--ec-parity-units", "0"], "--ec-parity-units"),
     (["--non-persistent-local-ckpt-dir", "/x", "--ec-unit-bytes", "1000"], "--ec-unit-bytes"),
     (["--non-persistent-local-ckpt-dir", "/x", "--ec-jump", "0"], "--ec-jump"),

@@ -424,3 +424,40 @@ def test_flat_buffer_cut_into_odd_shards(pkg, dev, n):
                            par[0], None, par[2]], k, m)
     assert _eq(rec[0], d[0]) and _eq(rec[2], d[2]) and _eq(rec[7], oracle.rs_encode(
         oracle.cauchy(k, m), d)[1])
+
+
+@pytest.mark.parametrize("k,m,unit,lost", [(20, 6, 4096, (0, 5, 19, 20, 23, 25)),
+                                           (5, 9, 1024, (1, 2, 6, 13)),
+                                           (32, 16, 8192, (0, 31, 32, 47))])
+def test_batched_wide_codes(pkg, dev, k, m, unit, lost):
+    """Batched encode, decode and update for codes past the fixed-size
+    kernels, on ragged and misaligned tensor lists, against the oracle."""
+    rng = np.random.default_rng(k * 100 + m)
+    host, tensors = _ragged_device(rng, dev, 3 * k, 3 * unit, misalign=(k == 5))
+    pset = pkg.encode(tensors, k, m, unit)
+    torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(), _oracle_layout_parity(pset.layout, host, unit))
+    lay = pset.layout
+    par_ref = pset.parity.clone()
+    for s in range(lay.n_stripes):
+        for pos in lost:
+            u = s * k + pos
+            if pos < k and u < lay.n_units:
+                lay.unit_view(u).fill_(0xA5)
+            elif pos >= k:
+                pset.parity[s, pos - k].fill_(0x5A)
+    pkg.decode(pset, lost)
+    torch.cuda.synchronize()
+    for h, t in zip(host, tensors):
+        assert np.array_equal(t.cpu().numpy(), h)
+    assert torch.equal(pset.parity, par_ref)
+    changed = np.sort(rng.choice(lay.n_units, max(1, lay.n_units // 7), replace=False))
+    olds = []
+    for u in changed:
+        v = lay.unit_view(int(u))
+        olds.append(v.clone())
+        v.copy_(torch.from_numpy(rng.integers(0, 256, v.numel(), dtype=np.uint8)))
+    pkg.update(pset, changed, olds)
+    fresh = lay.encode()
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity, fresh)
