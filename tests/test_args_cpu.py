@@ -2,7 +2,6 @@
 local checkpoints (megatron/training/arguments.py:1049-1056, :2126-2133,
 :2422-2431), and the checkpointing context of training.py:806-838."""
 import argparse
-import os
 import socket
 
 import pytest

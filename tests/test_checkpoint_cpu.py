@@ -5,7 +5,6 @@ test_replication.py:144-160 (lose some ranks' local data, still load the
 iteration), test_local.py:246-326 (a failed save raises everywhere and leaves
 nothing), test_local.py:225-244 (a new save removes the older one)."""
 import glob
-import os
 import socket
 
 import pytest
