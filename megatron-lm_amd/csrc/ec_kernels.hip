@@ -14,8 +14,9 @@
 //   The m parity outputs of those bytes are accumulated in VGPRs and written
 //   once: every input byte is read from HBM exactly once and every parity
 //   byte written exactly once.  Loads and stores are non-temporal (streamed
-//   past L2 and the Infinity Cache), and tiles are renumbered so that the
-//   shards are streamed at two places at once (split_tile).  Measured on
+//   past L2 and the Infinity Cache), and for shards below 512 MiB tiles are
+//   renumbered so that the shards are streamed at two places at once
+//   (tile_order).  Measured on
 //   MI355X for RS(6,3) over 256 MiB shards: plain loads/stores and tables in
 //   SGPRs 5.48 TB/s of HBM traffic; streaming access 5.90; plus LDS tables
 //   6.15; the two-place order with one chunk per lane 6.29-6.54 over five
@@ -122,13 +123,24 @@ __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
 // XCDs (workgroup b runs on XCD b % 8).  Renumbering b -> (b % 2) * per + b / 2
 // gives the even XCDs the first half of the tile range and the odd XCDs the
 // second half, so every shard is streamed at two places half a shard apart.
-// On MI355X this beat launch order (one place) and one window per XCD (eight
-// places) for every code measured, on every buffer layout tried: separate
-// allocations, one packed block, random 4 KiB offsets, 1 MiB and 12 KiB
-// padding.  A bijection on [0, gridDim.x); an odd last tile keeps its index.
+// On MI355X, for shards below kSplitMaxBytes, this beat launch order (one
+// place) and one window per XCD (eight places) for every code measured, on
+// every buffer layout tried: separate allocations, one packed block, random
+// 4 KiB offsets, 1 MiB and 12 KiB padding.  From 512 MiB shards on it lost
+// 8-20 % to launch order (RS(6,3): 512 MiB 4.80 vs 5.65 TB/s, 1 GiB 4.93 vs
+// 5.92, 2 GiB 5.06 vs 5.73; up to 448 MiB it won or tied), also with the
+// halves interleaved in segments of 16-256 MiB, so larger shards keep
+// launch order.  A bijection on [0, gridDim.x); an odd last tile keeps its
+// index.
+constexpr uint64_t kSplitMaxBytes = 512ull << 20;
+
 __device__ __forceinline__ uint32_t split_tile(uint32_t b, uint32_t nb) {
   const uint32_t per = nb >> 1;
   return b < (per << 1) ? (b & 1u) * per + (b >> 1) : b;
+}
+
+__device__ __forceinline__ uint32_t tile_order(uint32_t b, uint32_t nb, uint64_t n16) {
+  return n16 * 16 < kSplitMaxBytes ? split_tile(b, nb) : b;
 }
 
 // Copy the m x k permute tables from the kernel arguments into LDS, where
@@ -262,7 +274,7 @@ __global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
   stage_tables<K, M>(tab, a.tab);
   const uint64_t tile = (uint64_t)kBlock * U;
   const uint64_t stride = (uint64_t)gridDim.x * tile;
-  for (uint64_t base = (uint64_t)split_tile(blockIdx.x, gridDim.x) * tile + threadIdx.x;
+  for (uint64_t base = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * tile + threadIdx.x;
        base < a.n16; base += stride) {
     uint4 x[U][K];
 #pragma unroll
@@ -451,7 +463,7 @@ __global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
   for (int t = threadIdx.x; t < M * k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
   __syncthreads();
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)split_tile(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
+  for (uint64_t idx = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * kBlock + threadIdx.x;
        idx < a.n16; idx += stride) {
     uint32_t acc[M][4] = {};
     for (int j0 = 0; j0 < k; j0 += kWideGroup) {
