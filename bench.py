@@ -375,7 +375,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
-    ap.add_argument("--mode", choices=["full", "headline", "pmc", "batched", "batched-pmc"],
+    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched", "batched-pmc"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
@@ -442,6 +442,11 @@ def main() -> int:
         raise AssertionError("decode did not reproduce the lost shards")
     dec_gbs = data_bytes / (dwall * 1e-3) / 1e9
     log(f"decode lost={lost}: {dec_gbs:.1f} GB/s data")
+    if args.mode == "decode":
+        print(json.dumps({"mode": "decode", "lost": lost, "decode_GBps": round(dec_gbs, 2),
+                          "kernel_us": round(dev_ms * 1e3, 2),
+                          "traffic_GBps": round(traffic / (dev_ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
 
     # ---- config 1: XOR, 4 x 64 MiB bf16 ----------------------------------
     xh = synth.xor_shards(args.seed, 64 * MiB, 4)
