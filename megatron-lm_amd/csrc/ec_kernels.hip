@@ -603,8 +603,38 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
   }
 }
 
+// A full tile whose units are not all 16-byte aligned (tensors that are
+// views into a flat buffer at arbitrary offsets): one chunk per lane at a
+// time, each unit read through load_realign (two aligned loads and a byte
+// shift for a misaligned unit); the outputs are aligned.
+template <int K, int M, int U>
+__device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K],
+                                                  uint8_t* const (&dst)[M],
+                                                  const PermTab (&tab)[M][K]) {
+  constexpr int V = U >= 2 ? 2 : 1;  // chunks per lane in flight together
+#pragma unroll 1
+  for (int u0 = 0; u0 < U; u0 += V) {
+    uint4 x[V][K];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+#pragma unroll
+      for (int j = 0; j < K; ++j) x[v][j] = load_realign(src[j], rel);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+      uint32_t acc[M][4] = {};
+      gf_matvec16<K, M>(acc, x[v], tab);
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  }
+}
+
 // Any other tile (a unit or output ending inside it, an absent unit, a
-// misaligned address): one unit at a time, descriptors re-read from memory,
+// misaligned output): one unit at a time, descriptors re-read from memory,
 // byte-granular at the ends.  Kept as a rolled loop so that its registers
 // stay below the fast path's (the allocator takes the larger of the two).
 template <int K, int M, int U>
@@ -655,13 +685,13 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
   // whether everything is 16-byte aligned.
   const uint8_t* d[K];
   uint32_t len[K];
-  bool aligned = true;
+  bool in_aligned = true, out_aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
     const uint32_t l = d[j] ? a.dlen[(uint64_t)s * K + j] : 0u;
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    aligned &= (reinterpret_cast<uintptr_t>(d[j]) & 15u) == 0;
+    in_aligned &= (reinterpret_cast<uintptr_t>(d[j]) & 15u) == 0;
   }
   uint8_t* p[M];
   uint32_t olen[M];
@@ -670,7 +700,7 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
     p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
     const uint32_t l = p[i] ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
     olen[i] = l < a.unit_bytes ? l : a.unit_bytes;
-    aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+    out_aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
   }
   constexpr uint32_t kTileBytes = kBlock * U * 16u;
   for (uint32_t t = t0; t < t1; ++t) {
@@ -680,7 +710,7 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
     // output does not cover it.
     const uint8_t* src[K];
     uint8_t* dst[M];
-    bool edge = !aligned;
+    bool edge = !out_aligned;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       src[j] = len[j] >= hi ? d[j] + lo : g_zero_tile;
@@ -691,10 +721,12 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
       dst[i] = p[i] + lo;
       edge |= olen[i] < hi;
     }
-    if (!edge)
+    if (edge)
+      tile_edge<K, M, U>(a, s, base, tab);
+    else if (in_aligned)
       tile_full<K, M, U>(src, dst, tab);
     else
-      tile_edge<K, M, U>(a, s, base, tab);
+      tile_full_realign<K, M, U>(src, dst, tab);
   }
 }
 
