@@ -766,11 +766,10 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     od[j] = nw[j] ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]) : nullptr;
     const uint32_t l = nw[j] ? a.len[(uint64_t)s * K + j] : 0u;
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    if (nw[j]) {
-      full = len[j] < full ? len[j] : full;
-      aligned &= ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
-    }
+    if (nw[j]) full = len[j] < full ? len[j] : full;
   }
+  // Misaligned units (views at arbitrary offsets) are realigned on the fast
+  // path (load_realign); only the parity must be 16-byte aligned for it.
   uint8_t* p[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
@@ -793,8 +792,8 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     for (int j = 0; j < K; ++j) {
       if (nw[j] == nullptr) continue;  // uniform: unchanged unit
       if (!fast && off >= len[j]) continue;
-      const uint4 vn = fast ? load_stream(nw[j] + off) : load_unit(nw[j], off, len[j]);
-      const uint4 vo = fast ? load_stream(od[j] + off) : load_unit(od[j], off, len[j]);
+      const uint4 vn = fast ? load_realign(nw[j], off) : load_unit(nw[j], off, len[j]);
+      const uint4 vo = fast ? load_realign(od[j], off) : load_unit(od[j], off, len[j]);
       const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
       Fields f[4];
 #pragma unroll

@@ -251,7 +251,11 @@ def _oracle_layout_parity(layout, host, unit):
 
 
 @pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 4096, False), (8, 2, 1024, True),
-                                               (6, 3, 65536, False), (5, 1, 256, True)])
+                                               (6, 3, 65536, False), (5, 1, 256, True),
+                                               # misaligned units with full tiles: the
+                                               # realigning fast path
+                                               (12, 4, 4096, True), (8, 2, 16384, True),
+                                               (6, 3, 65536, True), (3, 2, 32768, True)])
 def test_batched_encode_matches_oracle(pkg, dev, k, m, unit, misalign):
     rng = np.random.default_rng(k * 7 + unit)
     host, tensors = _ragged_device(rng, dev, 40, 6 * unit, misalign)
@@ -320,10 +324,11 @@ def test_batched_decode_stripe_subset(pkg, dev):
     assert lay.plan_decode(pset.parity, [1], stripes=[]) is None
 
 
-@pytest.mark.parametrize("k,m,unit", [(12, 4, 2048), (6, 3, 20480)])
-def test_batched_update_equals_reencode(pkg, dev, k, m, unit):
+@pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 2048, False), (6, 3, 20480, False),
+                                                (12, 4, 4096, True), (8, 2, 16384, True)])
+def test_batched_update_equals_reencode(pkg, dev, k, m, unit, misalign):
     rng = np.random.default_rng(77 + k)
-    host, tensors = _ragged_device(rng, dev, 60, 8 * unit)
+    host, tensors = _ragged_device(rng, dev, 60, 8 * unit, misalign)
     pset = pkg.encode(tensors, k, m, unit)
     lay = pset.layout
     changed = np.sort(rng.choice(lay.n_units, max(1, lay.n_units // 10), replace=False))
