@@ -759,17 +759,23 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
   const uint8_t* od[K];
   uint32_t len[K];
   uint32_t full = a.unit_bytes;
-  bool aligned = true;
+  bool aligned = true, in_aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     nw[j] = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
     od[j] = nw[j] ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]) : nullptr;
     const uint32_t l = nw[j] ? a.len[(uint64_t)s * K + j] : 0u;
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    if (nw[j]) full = len[j] < full ? len[j] : full;
+    if (nw[j]) {
+      full = len[j] < full ? len[j] : full;
+      in_aligned &=
+          ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
+    }
   }
   // Misaligned units (views at arbitrary offsets) are realigned on the fast
-  // path (load_realign); only the parity must be 16-byte aligned for it.
+  // path (load_realign); only the parity must be 16-byte aligned for it.  The
+  // aligned case keeps plain loads: realigning every load cost the 1 %
+  // update 5 % (0.338 -> 0.356 ms).
   uint8_t* p[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
@@ -792,8 +798,17 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     for (int j = 0; j < K; ++j) {
       if (nw[j] == nullptr) continue;  // uniform: unchanged unit
       if (!fast && off >= len[j]) continue;
-      const uint4 vn = fast ? load_realign(nw[j], off) : load_unit(nw[j], off, len[j]);
-      const uint4 vo = fast ? load_realign(od[j], off) : load_unit(od[j], off, len[j]);
+      uint4 vn, vo;
+      if (fast && in_aligned) {
+        vn = load_stream(nw[j] + off);
+        vo = load_stream(od[j] + off);
+      } else if (fast) {
+        vn = load_realign(nw[j], off);
+        vo = load_realign(od[j], off);
+      } else {
+        vn = load_unit(nw[j], off, len[j]);
+        vo = load_unit(od[j], off, len[j]);
+      }
       const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
       Fields f[4];
 #pragma unroll
