@@ -172,35 +172,47 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
 
 def checkpoint_staging(pkg, tensors) -> dict:
     """The save and load sides of the erasure-coded checkpoint manager on one
-    GPU, for config 5's tensors: encode into k + m slices and stage them to
-    pinned host memory (one transfer), and back: k slices with two data
-    positions missing to rebuilt tensors.  Data GB/s over wall time; the
-    second call of each is timed (the first pins the host buffers)."""
+    GPU, for config 5's tensors: encode into k + m slices staged to host
+    memory through 1 GiB pinned chunks, and back: k slices with two data
+    positions missing to rebuilt tensors.  Data GB/s over wall time.  The
+    first encode writes a fresh host array (page faults and zeroing on first
+    touch: the "cold" rate); the next ones reuse it, as repeated saves do.
+    The transfers share the host's PCIe and memory with other tenants, so the
+    median of three calls is reported for each direction."""
+    import statistics
     import torch
     from megatron_lm_amd.checkpoint import GpuSliceCodec
     codec = GpuSliceCodec(12, 4, 64 << 10)
     nbytes = sum(t.numel() * t.element_size() for t in tensors)
+    dev = tensors[0].device
     try:
-        codec.encode(tensors)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        meta, slices = codec.encode(tensors)
-        t_enc = time.perf_counter() - t0
-        keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
-        keep = dict(list(sorted(keep.items()))[:12])
-        dev = tensors[0].device
-        del slices
-        codec.decode(meta, keep, dev)
-        t0 = time.perf_counter()
-        rebuilt = codec.decode(meta, keep, dev)
-        t_dec = time.perf_counter() - t0
-        ok = all(torch.equal(a.view(-1).view(torch.uint8), b.view(-1).view(torch.uint8))
-                 for a, b in zip(rebuilt, tensors))
-        if not ok:
-            raise AssertionError("checkpoint decode did not rebuild the tensors")
-        del rebuilt, keep
-        res = {"ckpt_encode_to_host_GBps": round(nbytes / t_enc / 1e9, 1),
-               "ckpt_decode_from_host_GBps": round(nbytes / t_dec / 1e9, 1)}
+        codec.encode(tensors)                # result dropped: the host array is free again
+        t_cold = time.perf_counter() - t0
+        t_enc, keep = [], None
+        for _ in range(3):
+            keep = None                      # the last call's slices free the host array
+            t0 = time.perf_counter()
+            meta, slices = codec.encode(tensors)
+            t_enc.append(time.perf_counter() - t0)
+            keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
+            keep = dict(list(sorted(keep.items()))[:12])
+            del slices
+        t_dec = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            rebuilt = codec.decode(meta, keep, dev)
+            t_dec.append(time.perf_counter() - t0)
+            ok = all(torch.equal(a.view(-1).view(torch.uint8), b.view(-1).view(torch.uint8))
+                     for a, b in zip(rebuilt, tensors))
+            if not ok:
+                raise AssertionError("checkpoint decode did not rebuild the tensors")
+            del rebuilt
+        del keep
+        res = {"ckpt_encode_to_host_GBps": round(nbytes / statistics.median(t_enc) / 1e9, 1),
+               "ckpt_encode_to_host_cold_GBps": round(nbytes / t_cold / 1e9, 1),
+               "ckpt_decode_from_host_GBps": round(nbytes / statistics.median(t_dec) / 1e9, 1)}
     except RuntimeError as e:  # pinned-memory limits differ between hosts
         res = {"ckpt_staging_error": str(e)[:200]}
     log(f"checkpoint staging: {res}")

@@ -50,6 +50,7 @@ import io
 import json
 import os
 import re
+import sys
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -111,23 +112,54 @@ class GpuSliceCodec:
     """Encode a rank's tensors into k + m slices and back, on the GPU.
 
     Slice p is the concatenation over stripes of codeword position p (units
-    zero-padded to ``unit_bytes``): n_stripes * unit_bytes bytes.  Encode
-    builds all k + m slices in one device block (the parity kernel writes its
-    units straight into the parity slices, one gather launch copies the data
-    units into theirs) and moves the block to pinned host memory in one
-    transfer.  Decode moves the k slices it got back in one transfer, scatters
-    the data slices into fresh tensors in one launch, and rebuilds the lost
-    data positions from the k slices in one more.  The returned host slices
-    are views of one pinned buffer."""
+    zero-padded to ``unit_bytes``): n_stripes * unit_bytes bytes, returned as
+    rows of one pageable host array.
 
-    def __init__(self, k: int, m: int, unit_bytes: int):
+    Both directions work in chunks of stripes of at most ``chunk_bytes``,
+    double-buffered on the device and in pinned host memory, so a checkpoint
+    needs 2 * chunk_bytes of extra HBM and of page-locked memory, not
+    (k + m) / k of the state.
+
+    The codec keeps the host array of its last encode and writes the next
+    encode of the same shape into it once no slice of it is referenced any
+    more (the slices are views, so they hold the array): a fresh array costs
+    the kernel's page faults and zeroing on first touch, which on a 27 GB
+    checkpoint halves the staging rate.
+
+    Encode, per chunk: the parity kernel writes the parity units into the
+    device buffer's parity rows and one k = m = 1 gather launch copies the
+    data units into its data rows; the buffer goes to pinned memory on a copy
+    stream, and a thread pool moves it into the result while the next chunk
+    is coded and transferred.  Decode, per chunk: the thread pool copies the k
+    slices' part into pinned memory, the copy stream sends it up, one scatter
+    launch puts the data rows into fresh tensors and one decode launch
+    rebuilds the lost data positions; the next chunk's host copy overlaps."""
+
+    def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30):
         from . import layout as _layout
         self._layout = _layout
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
+        self.chunk_bytes = chunk_bytes
+        self._host: Optional[np.ndarray] = None
+
+    def _host_out(self, shape: Tuple[int, int]) -> np.ndarray:
+        """The previous encode's host array when it has this shape and no
+        view of it is alive, else a new one (which replaces it)."""
+        buf = self._host
+        # references: self._host, buf, getrefcount's argument; a live slice adds one
+        if buf is not None and buf.shape == shape and sys.getrefcount(buf) == 3:
+            return buf
+        self._host = buf = None
+        self._host = np.empty(shape, np.uint8)
+        return self._host
+
+    def _chunk_stripes(self, n_stripes: int, rows: int) -> int:
+        return max(1, min(n_stripes, self.chunk_bytes // (rows * self.unit_bytes)))
 
     @staticmethod
     def _rows(block: torch.Tensor, p: int) -> np.ndarray:
-        """Device addresses of the n_stripes units of slice p of a block."""
+        """Device addresses of the units of row p of a (rows, stripes,
+        unit_bytes) device block."""
         S, U = block.shape[1], block.shape[2]
         return np.uint64(block[p].data_ptr()) + np.arange(S, dtype=np.uint64) * np.uint64(U)
 
@@ -135,31 +167,78 @@ class GpuSliceCodec:
     def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
 
+    @staticmethod
+    def _pieces(rows: int, c0: int, c: int, U: int):
+        """(row, first byte, end byte) pieces of at most 64 MiB covering
+        stripes [c0, c0 + c) of every row."""
+        return [(r, a, min(a + (64 << 20), (c0 + c) * U))
+                for r in range(rows) for a in range(c0 * U, (c0 + c) * U, 64 << 20)]
+
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         from . import _lib
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
+        tensors = list(tensors)
         lay = self._layout.StripeLayout(tensors, k, m, U)
         S, dev = lay.n_stripes, lay.device
-        block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
-        # parity unit (s, i) goes to row s of slice k + i
-        pptr = np.stack([self._rows(block, k + i) for i in range(m)], axis=1)
-        pptr = self._dev(pptr, np.int64, dev)
-        _lib.check(_lib.lib().ec_encode_batched(
-            _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
-            pptr.data_ptr(), S, U, stream_handle(None, dev)), "ec_encode_batched")
-        # gather: every data unit (s, p) to row s of slice p, one k=m=1 launch
-        optr = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1), np.int64, dev)
+        C = self._chunk_stripes(S, k + m)
+        chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
+        nb = min(2, len(chunks))
+        out = self._host_out((k + m, S * U))
         one = np.ones((1, 1), np.uint8)
-        _lib.check(_lib.lib().ec_encode_batched(
-            _lib.u8ptr(one), 1, 1, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(), optr.data_ptr(),
-            S * k, U, stream_handle(None, dev)), "ec_encode_batched (gather)")
-        host = torch.empty((k + m, S, U), dtype=torch.uint8, pin_memory=True)
-        host.copy_(block, non_blocking=True)
-        torch.cuda.current_stream(dev).synchronize()
+        with torch.cuda.device(dev), \
+                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+            comp, copy = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
+            bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
+            pins = [torch.empty((k + m, C, U), dtype=torch.uint8, pin_memory=True)
+                    for _ in range(nb)]
+            # per buffer: parity unit (s, i) -> row k + i, data unit (s, p) -> row p
+            pp = [self._dev(np.stack([self._rows(b, k + i) for i in range(m)], axis=1), np.int64,
+                            dev) for b in bufs]
+            gp = [self._dev(np.stack([self._rows(b, p) for p in range(k)], axis=1), np.int64, dev)
+                  for b in bufs]
+            landed: List[torch.cuda.Event] = []   # chunk n is in pins[n % nb]
+            drained: List[list] = []              # host copies of chunk n out of pins
+
+            def drain(n):
+                c0, c = chunks[n]
+                flat = pins[n % nb].numpy().reshape(k + m, -1)
+                landed[n].synchronize()
+                return [pool.submit(np.copyto, out[r, a:b], flat[r, a - c0 * U:b - c0 * U])
+                        for r, a, b in self._pieces(k + m, c0, c, U)]
+
+            for n, (c0, c) in enumerate(chunks):
+                b = n % nb
+                if n >= nb:
+                    comp.wait_event(landed[n - nb])    # device buffer b is free again
+                dp = lay.d_ptrs.data_ptr() + c0 * k * 8
+                dl = lay.d_len.data_ptr() + c0 * k * 4
+                _lib.check(_lib.lib().ec_encode_batched(
+                    _lib.u8ptr(lay.coeff), k, m, dp, dl, pp[b].data_ptr(), c, U,
+                    stream_handle(comp, dev)), "ec_encode_batched")
+                _lib.check(_lib.lib().ec_encode_batched(
+                    _lib.u8ptr(one), 1, 1, dp, dl, gp[b].data_ptr(), c * k, U,
+                    stream_handle(comp, dev)), "ec_encode_batched (gather)")
+                ready = torch.cuda.Event()
+                ready.record(comp)
+                if n >= nb:
+                    for f in drained[n - nb]:           # pinned buffer b is free again
+                        f.result()
+                copy.wait_event(ready)
+                with torch.cuda.stream(copy):  # row by row: each row's part is contiguous
+                    for r in range(k + m):
+                        pins[b][r, :c].copy_(bufs[b][r, :c], non_blocking=True)
+                landed.append(torch.cuda.Event())
+                landed[-1].record(copy)
+                if n >= 1:
+                    drained.append(drain(n - 1))      # overlaps chunk n's transfer
+            drained.append(drain(len(chunks) - 1))
+            for fs in drained[-nb:]:
+                for f in fs:
+                    f.result()
         meta = {"k": k, "m": m, "unit_bytes": U, "n_stripes": S, "n_units": lay.n_units,
                 "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
-        return meta, [host[p].numpy().reshape(-1) for p in range(k + m)]
+        return meta, [out[p] for p in range(k + m)]
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib
@@ -176,57 +255,80 @@ class GpuSliceCodec:
         lay = self._layout.StripeLayout(tensors, k, m, U, device=device)
         if lay.n_stripes != S or lay.n_units != meta["n_units"]:
             raise CheckpointingException("checkpoint header does not match its tensors")
-        host = torch.empty((k, S, U), dtype=torch.uint8, pin_memory=True)
-        block = torch.empty((k, S, U), dtype=torch.uint8, device=device)
-        # Copy the slices into the pinned block in 64 MiB pieces on a thread
-        # pool (numpy releases the GIL for large copies; one thread moves
-        # ~10 GB/s), and start each piece's host-to-device transfer as soon as
-        # the piece is in place, so the copies overlap the transfer.
-        pieces = [(r, a, min(a + (64 << 20), S * U)) for r in range(k)
-                  for a in range(0, S * U, 64 << 20)]
-        flat = host.numpy().reshape(k, -1)
-        hflat, dflat = host.view(k, -1), block.view(k, -1)
-
-        def put(piece):
-            r, a, b = piece
-            flat[r, a:b] = slices[avail[r]][a:b]
-        with torch.cuda.device(device), \
-                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
-            for piece, done in zip(pieces, [pool.submit(put, pc) for pc in pieces]):
-                done.result()
-                r, a, b = piece
-                dflat[r, a:b].copy_(hflat[r, a:b], non_blocking=True)
-        one = np.ones((1, 1), np.uint8)
-        # scatter the data slices we have into the tensors, one k=m=1 launch
         have = [(r, p) for r, p in enumerate(avail) if p < k]
-        if have:
-            sptr = np.concatenate([self._rows(block, r) for r, _ in have])
-            optr = np.concatenate([lay.host_ptrs[:, p] for _, p in have])
-            olen = np.concatenate([lay.host_len[:, p] for _, p in have])
-            args = [self._dev(sptr, np.int64, device),
-                    torch.full((sptr.size,), U, dtype=torch.int32, device=device),
-                    self._dev(optr, np.int64, device), self._dev(olen, np.int32, device)]
-            _lib.check(_lib.lib().ec_decode_batched(
-                _lib.u8ptr(one), 1, 1, *[t.data_ptr() for t in args], sptr.size, U,
-                stream_handle(None, device)), "ec_decode_batched (scatter)")
-        # rebuild the missing data positions from the k slices, one launch
-        lost_data = [p for p in range(k) if p not in slices or p not in avail]
+        lost_data = [p for p in range(k) if p not in avail]
+        rows = None
         if lost_data:
             erased = [p for p in range(k + m) if p not in avail]
             surv, rows = decode_matrix(lay.coeff, erased)
             if surv != avail:
                 raise CheckpointingException("decode plan does not match the slices read")
-            pick = [erased.index(p) for p in lost_data]
-            rows = np.ascontiguousarray(rows[pick])
-            sptr = np.stack([self._rows(block, r) for r in range(k)], axis=1)
-            args = [self._dev(sptr, np.int64, device),
-                    torch.full((S, k), U, dtype=torch.int32, device=device),
-                    self._dev(lay.host_ptrs[:, lost_data], np.int64, device),
-                    self._dev(lay.host_len[:, lost_data], np.int32, device)]
-            _lib.check(_lib.lib().ec_decode_batched(
-                _lib.u8ptr(rows), k, len(lost_data), *[t.data_ptr() for t in args], S, U,
-                stream_handle(None, device)), "ec_decode_batched")
-        torch.cuda.current_stream(device).synchronize()
+            rows = np.ascontiguousarray(rows[[erased.index(p) for p in lost_data]])
+        C = self._chunk_stripes(S, k)
+        chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
+        nb = min(2, len(chunks))
+        one = np.ones((1, 1), np.uint8)
+        hp = [p for _, p in have]
+        with torch.cuda.device(device), \
+                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+            comp, copy = torch.cuda.current_stream(device), torch.cuda.Stream(device)
+            bufs = [torch.empty((k, C, U), dtype=torch.uint8, device=device) for _ in range(nb)]
+            pins = [torch.empty((k, C, U), dtype=torch.uint8, pin_memory=True)
+                    for _ in range(nb)]
+            # Every descriptor array is uploaded once, stripe-major, so that a
+            # chunk's descriptors are a contiguous slice (a pointer offset).
+            full = torch.full((C * k,), U, dtype=torch.int32, device=device)
+            scat_src = [self._dev(np.stack([self._rows(bf, r) for r, _ in have], axis=1)
+                                  if have else np.zeros(1, np.uint64), np.int64, device)
+                        for bf in bufs]
+            scat_dst = self._dev(lay.host_ptrs[:, hp], np.int64, device)
+            scat_len = self._dev(lay.host_len[:, hp], np.int32, device)
+            dec_src = [self._dev(np.stack([self._rows(bf, r) for r in range(k)], axis=1),
+                                 np.int64, device) for bf in bufs]
+            dec_dst = self._dev(lay.host_ptrs[:, lost_data], np.int64, device)
+            dec_len = self._dev(lay.host_len[:, lost_data], np.int32, device)
+            sent: List[torch.cuda.Event] = []      # chunk n has left pins[n % nb]
+            consumed: List[torch.cuda.Event] = []  # chunk n is decoded out of bufs[n % nb]
+
+            def fill(n):
+                c0, c = chunks[n]
+                flat = pins[n % nb].numpy().reshape(k, -1)
+                return [pool.submit(np.copyto, flat[r, a - c0 * U:b - c0 * U],
+                                    slices[avail[r]][a:b])
+                        for r, a, b in self._pieces(k, c0, c, U)]
+
+            filling = fill(0)
+            for n, (c0, c) in enumerate(chunks):
+                b = n % nb
+                for f in filling:
+                    f.result()
+                if n >= nb:
+                    copy.wait_event(consumed[n - nb])  # device buffer b is free again
+                with torch.cuda.stream(copy):  # row by row: each row's part is contiguous
+                    for r in range(k):
+                        bufs[b][r, :c].copy_(pins[b][r, :c], non_blocking=True)
+                sent.append(torch.cuda.Event())
+                sent[-1].record(copy)
+                comp.wait_event(sent[-1])
+                if have:  # the data slices we have go into the tensors
+                    h = len(have)
+                    _lib.check(_lib.lib().ec_decode_batched(
+                        _lib.u8ptr(one), 1, 1, scat_src[b].data_ptr(), full.data_ptr(),
+                        scat_dst.data_ptr() + c0 * h * 8, scat_len.data_ptr() + c0 * h * 4,
+                        c * h, U, stream_handle(comp, device)), "ec_decode_batched (scatter)")
+                if lost_data:  # rebuild the missing data positions from the k rows
+                    nl = len(lost_data)
+                    _lib.check(_lib.lib().ec_decode_batched(
+                        _lib.u8ptr(rows), k, nl, dec_src[b].data_ptr(), full.data_ptr(),
+                        dec_dst.data_ptr() + c0 * nl * 8, dec_len.data_ptr() + c0 * nl * 4,
+                        c, U, stream_handle(comp, device)), "ec_decode_batched")
+                consumed.append(torch.cuda.Event())
+                consumed[-1].record(comp)
+                if n + 1 < len(chunks):
+                    if n + 1 >= nb:
+                        sent[n + 1 - nb].synchronize()  # pinned buffer is free again
+                    filling = fill(n + 1)               # overlaps chunk n's transfer
+            comp.synchronize()
         return tensors
 
 
