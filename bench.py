@@ -99,7 +99,7 @@ def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host
     }
 
 
-def batched_configs(pkg, synth, dev, seed: int) -> dict:
+def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad") -> dict:
     """Configs 4 and 5 through the batched stripe launcher: data GB/s of one
     launch (HIP events) and HBM traffic GB/s, with product-only checks (a
     decode round trip; update == full re-encode)."""
@@ -165,6 +165,7 @@ def batched_configs(pkg, synth, dev, seed: int) -> dict:
     del lay, par, olds, plan, dplan
     torch.cuda.empty_cache()
     out.update(checkpoint_staging(pkg, tensors))
+    out.update(checkpoint_snapshot(pkg, tensors, gemm))
     del tensors
     torch.cuda.empty_cache()
     return out
@@ -219,49 +220,129 @@ def checkpoint_staging(pkg, tensors) -> dict:
     return res
 
 
-def overlap_with_training(pkg, dev, data, parity, coeff) -> dict:
-    """Checkpoint encode concurrent with a training-like load: 8192^3 bf16
-    GEMMs on torch's stream, the RS(6,3) encode on a side stream of default
-    priority.  Reports each one alone and both together (HIP events on each
-    stream), so the interference on training is visible."""
+class GemmLoad:
+    """A training-like load: 8192^3 bf16 GEMMs on torch's current stream."""
+    N = 8192
+
+    def __init__(self, dev):
+        import torch
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        self.a = torch.randn(self.N, self.N, device=dev, dtype=torch.bfloat16, generator=g)
+        self.b = torch.randn(self.N, self.N, device=dev, dtype=torch.bfloat16, generator=g)
+        self.c = torch.empty(self.N, self.N, device=dev, dtype=torch.bfloat16)
+        self.flops = 2 * self.N ** 3
+
+    def enqueue(self, n: int):
+        """n GEMMs bracketed by timing events on the current stream."""
+        import torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            torch.matmul(self.a, self.b, out=self.c)
+        e1.record()
+        return e0, e1
+
+    def ms_alone(self, n: int = 30) -> float:
+        import torch
+        self.enqueue(3)
+        torch.cuda.synchronize()
+        e0, e1 = self.enqueue(n)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+
+def overlap_with_training(pkg, dev, data, parity, coeff, gemm: "GemmLoad") -> dict:
+    """Checkpoint encode concurrent with a training-like load: GEMMs on
+    torch's stream, the RS(6,3) encode beside them on (a) the engine's side
+    stream, which has a hardware queue of its own, and (b) a stream from
+    torch's pool, which shares a queue with torch's stream.  Default priority
+    both.  The encode is sized to outlast the GEMM window, so the GEMM's time
+    per call is measured under load throughout (HIP events on each stream)."""
     import torch
-    g = torch.Generator(device=dev)
-    g.manual_seed(1)
-    a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16, generator=g)
-    b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16, generator=g)
-    c = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
-    side = torch.cuda.Stream(device=dev)
-    n_gemm, n_enc = 30, 120
+    n_gemm = 60
+    g_alone = gemm.ms_alone()
 
-    def run(do_gemm, do_enc):
-        main = torch.cuda.current_stream()
-        ev = {k: torch.cuda.Event(enable_timing=True) for k in ("g0", "g1", "e0", "e1")}
+    def enc_ms(side, n):
         torch.cuda.synchronize()
-        if do_enc:
-            ev["e0"].record(side)
-            for _ in range(n_enc):
-                pkg.matvec(coeff, data, out=parity, stream=side)
-            ev["e1"].record(side)
-        if do_gemm:
-            ev["g0"].record(main)
-            for _ in range(n_gemm):
-                torch.matmul(a, b, out=c)
-            ev["g1"].record(main)
-        torch.cuda.synchronize()
-        return (ev["g0"].elapsed_time(ev["g1"]) / n_gemm if do_gemm else None,
-                ev["e0"].elapsed_time(ev["e1"]) / n_enc if do_enc else None)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        for _ in range(n):
+            pkg.matvec(coeff, data, out=parity, stream=side)
+        e1.record(side)
+        return e0, e1
 
-    run(True, True)  # warm-up of both
-    g_alone, _ = run(True, False)
-    _, e_alone = run(False, True)
-    g_both, e_both = run(True, True)
-    flops = 2 * 8192 ** 3
+    out = {"overlap_gemm_ms_alone": round(g_alone, 3),
+           "overlap_gemm_TFLOPs_alone": round(gemm.flops / g_alone / 1e9, 1)}
     data_bytes = sum(t.numel() for t in data)
-    return {"overlap_gemm_ms_alone": round(g_alone, 3),
-            "overlap_gemm_ms_with_encode": round(g_both, 3),
-            "overlap_gemm_TFLOPs_alone": round(flops / g_alone / 1e9, 1),
-            "overlap_encode_GBps_alone": round(data_bytes / e_alone / 1e6, 1),
-            "overlap_encode_GBps_with_gemm": round(data_bytes / e_both / 1e6, 1)}
+    for tag, side in (("", pkg.side_stream(dev)), ("_pooled_stream", torch.cuda.Stream(device=dev))):
+        e0, e1 = enc_ms(side, 20)
+        torch.cuda.synchronize()
+        e_alone = e0.elapsed_time(e1) / 20
+        n_enc = max(8, int(1.3 * n_gemm * g_alone / e_alone))
+        e0, e1 = enc_ms(side, n_enc)
+        g0, g1 = gemm.enqueue(n_gemm)
+        torch.cuda.synchronize()
+        g_both, e_both = g0.elapsed_time(g1) / n_gemm, e0.elapsed_time(e1) / n_enc
+        out[f"overlap_gemm_ms_with_encode{tag}"] = round(g_both, 3)
+        out[f"overlap_encode_GBps_alone{tag}"] = round(data_bytes / e_alone / 1e6, 1)
+        out[f"overlap_encode_GBps_with_gemm{tag}"] = round(data_bytes / e_both / 1e6, 1)
+    log(f"overlap: GEMM {g_alone:.3f} ms alone, {out['overlap_gemm_ms_with_encode']} ms beside "
+        f"the encode on the side stream, {out['overlap_gemm_ms_with_encode_pooled_stream']} ms "
+        f"on a pooled stream")
+    return out
+
+
+def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
+    """The save path that keeps training running, for config 5's tensors:
+    GpuSliceCodec.snapshot codes them into one HBM block on the side stream
+    and holds torch's stream only until that is done (the stall a save costs
+    training), then stages the block to host memory in a background thread
+    while GEMMs run on torch's stream.  Reports the stall, the staging time to
+    host memory, and the GEMM time per call during the staging next to its
+    time alone; the slices are checked against the synchronous encode's."""
+    import numpy as np
+    import torch
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    codec = GpuSliceCodec(12, 4, 64 << 10)
+    nbytes = sum(t.numel() * t.element_size() for t in tensors)
+    try:
+        g_alone = gemm.ms_alone()
+        codec.snapshot(tensors).result()         # warm: pinned buffers, host array
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pending = codec.snapshot(tensors)
+        mark = torch.cuda.Event()
+        mark.record()                 # torch's stream passes it once the coding is done
+        mark.synchronize()
+        t_stall = time.perf_counter() - t0
+        # about 0.25 s of GEMMs, enqueued at once so that no host gap enters
+        # their timing, inside the staging (which takes about twice as long)
+        n_gemm = max(10, int(0.25 / (g_alone * 1e-3)))
+        g0, g1 = gemm.enqueue(n_gemm)
+        g1.synchronize()
+        contained = not pending.done()
+        _, slices = pending.result()
+        t_staged = time.perf_counter() - t0
+        g_during = g0.elapsed_time(g1) / n_gemm
+        _, again = codec.encode(tensors)          # a second host array: slices is alive
+        # every parity byte, and the head of every data slice
+        if not all(np.array_equal(a, b) for a, b in zip(slices[12:], again[12:])) or \
+                not all(np.array_equal(a[:64 << 20], b[:64 << 20])
+                        for a, b in zip(slices[:12], again[:12])):
+            raise AssertionError("snapshot slices differ from the synchronous encode")
+        del again, slices
+        res = {"ckpt_snapshot_stall_ms": round(t_stall * 1e3, 2),
+               "ckpt_snapshot_stall_data_GBps": round(nbytes / t_stall / 1e9, 1),
+               "ckpt_snapshot_staged_s": round(t_staged, 3),
+               "ckpt_snapshot_gemm_ms_alone": round(g_alone, 3),
+               "ckpt_snapshot_gemm_ms_during_staging": round(g_during, 3),
+               "ckpt_snapshot_gemm_calls_during_staging": n_gemm,
+               "ckpt_snapshot_gemm_window_inside_staging": contained}
+    except RuntimeError as e:  # HBM or pinned-memory limits differ between hosts
+        res = {"ckpt_snapshot_error": str(e)[:200]}
+    log(f"checkpoint snapshot: {res}")
+    return res
 
 
 def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
@@ -412,7 +493,8 @@ def main() -> int:
     if args.mode == "pmc":
         return pmc_launches(pkg, dev)
     if args.mode == "batched":
-        print(json.dumps({"mode": "batched", **batched_configs(pkg, synth, dev, args.seed)}),
+        print(json.dumps({"mode": "batched",
+                          **batched_configs(pkg, synth, dev, args.seed, GemmLoad(dev))}),
               flush=True)
         return 0
     if args.mode == "batched-pmc":
@@ -473,10 +555,11 @@ def main() -> int:
     xor_gbs = 4 * 64 * MiB / (xwall * 1e-3) / 1e9
     log(f"XOR(4) {xor_gbs:.1f} GB/s data")
 
-    batched = {} if args.no_batched else batched_configs(pkg, synth, dev, args.seed)
+    gemm = GemmLoad(dev)
+    batched = {} if args.no_batched else batched_configs(pkg, synth, dev, args.seed, gemm)
     log("encode on a side stream vs bf16 GEMMs")
-    over = overlap_with_training(pkg, dev, data, parity, coeff)
-    log(f"overlap: {over}")
+    over = overlap_with_training(pkg, dev, data, parity, coeff, gemm)
+    del gemm
 
     # ---- practical ceiling: the engine's streaming copy (XOR of one shard,
     # same loads/stores as the kernels) and torch's device-to-device copy ---

@@ -16,13 +16,14 @@ Modules:
 from . import _lib
 from ._lib import ECError, ECLibraryMissing, SingularError
 from .codec import (cauchy_matrix, decode_matrix, gf_inv, gf_invert, gf_mul, matvec,
-                    reconstruct, rs_encode, xor_encode)
+                    reconstruct, rs_encode, side_stream, xor_encode)
 from .layout import StripeLayout
 from .api import ParitySet, decode, encode, update
 
 __all__ = [
     "ECError", "ECLibraryMissing", "SingularError", "cauchy_matrix", "decode_matrix",
-    "gf_inv", "gf_invert", "gf_mul", "matvec", "reconstruct", "rs_encode", "xor_encode",
+    "gf_inv", "gf_invert", "gf_mul", "matvec", "reconstruct", "rs_encode", "side_stream",
+    "xor_encode",
     "StripeLayout", "ParitySet", "encode", "decode", "update",
 ]
 

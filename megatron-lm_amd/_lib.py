@@ -37,6 +37,8 @@ EXPORTS = (
     "ec_encode_batched",
     "ec_decode_batched",
     "ec_parity_update",
+    "ec_stream_create",
+    "ec_stream_destroy",
 )
 
 
@@ -99,6 +101,10 @@ def lib() -> ctypes.CDLL:
     L.ec_decode_batched.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
     L.ec_parity_update.restype = _i
     L.ec_parity_update.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
+    L.ec_stream_create.restype = _i
+    L.ec_stream_create.argtypes = [_i, _i, ctypes.POINTER(_vp)]
+    L.ec_stream_destroy.restype = _i
+    L.ec_stream_destroy.argtypes = [_vp]
     _lib = L
     return L
 

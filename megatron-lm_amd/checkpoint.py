@@ -51,6 +51,7 @@ import json
 import os
 import re
 import sys
+import threading
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -108,6 +109,42 @@ def _dtype(name: str) -> torch.dtype:
 
 # ----------------------------------------------------------------- codec --
 
+class PendingSlices:
+    """The slices of a ``GpuSliceCodec.snapshot``, being staged to host memory
+    by a background thread.  ``coded`` is the device event after which the
+    tensors may change; ``meta`` is known at once; ``result()`` waits for the
+    staging and returns ``(meta, slices)`` (or raises what the staging
+    raised)."""
+
+    def __init__(self, meta: dict, coded: torch.cuda.Event, stage: Callable[[], list]):
+        self.meta, self.coded = meta, coded
+        self._slices: Optional[list] = None
+        self._error: Optional[BaseException] = None
+        self._done = threading.Event()
+        self._thread = threading.Thread(target=self._run, args=(stage,), daemon=True,
+                                        name="ec-stage")
+        self._thread.start()
+
+    def _run(self, stage) -> None:
+        try:
+            self._slices = stage()
+        except BaseException as e:  # noqa: BLE001 - handed to result()
+            self._error = e
+        finally:
+            self._done.set()
+
+    def done(self) -> bool:
+        return self._done.is_set()
+
+    def result(self, timeout: Optional[float] = None) -> Tuple[dict, List[np.ndarray]]:
+        if not self._done.wait(timeout):
+            raise TimeoutError("checkpoint slices still being staged")
+        self._thread.join()
+        if self._error is not None:
+            raise self._error
+        return self.meta, self._slices
+
+
 class GpuSliceCodec:
     """Encode a rank's tensors into k + m slices and back, on the GPU.
 
@@ -133,7 +170,14 @@ class GpuSliceCodec:
     is coded and transferred.  Decode, per chunk: the thread pool copies the k
     slices' part into pinned memory, the copy stream sends it up, one scatter
     launch puts the data rows into fresh tensors and one decode launch
-    rebuilds the lost data positions; the next chunk's host copy overlaps."""
+    rebuilds the lost data positions; the next chunk's host copy overlaps.
+
+    ``snapshot`` is the save path that keeps training running: it codes the
+    whole state into one HBM block (288 GB of HBM per MI355X holds a rank's
+    (k + m) / k copy) on a stream with its own hardware queue, holds torch's
+    stream only for those two launches, and stages the block to host memory
+    in a background thread while training goes on.  Transfers use that side
+    stream too, so they never queue behind (or in front of) training work."""
 
     def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30):
         from . import layout as _layout
@@ -141,17 +185,19 @@ class GpuSliceCodec:
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.chunk_bytes = chunk_bytes
         self._host: Optional[np.ndarray] = None
+        self._host_lock = threading.Lock()
 
     def _host_out(self, shape: Tuple[int, int]) -> np.ndarray:
         """The previous encode's host array when it has this shape and no
         view of it is alive, else a new one (which replaces it)."""
-        buf = self._host
-        # references: self._host, buf, getrefcount's argument; a live slice adds one
-        if buf is not None and buf.shape == shape and sys.getrefcount(buf) == 3:
-            return buf
-        self._host = buf = None
-        self._host = np.empty(shape, np.uint8)
-        return self._host
+        with self._host_lock:
+            buf = self._host
+            # references: self._host, buf, getrefcount's argument; a live slice adds one
+            if buf is not None and buf.shape == shape and sys.getrefcount(buf) == 3:
+                return buf
+            self._host = buf = None
+            self._host = np.empty(shape, np.uint8)
+            return self._host
 
     def _chunk_stripes(self, n_stripes: int, rows: int) -> int:
         return max(1, min(n_stripes, self.chunk_bytes // (rows * self.unit_bytes)))
@@ -174,9 +220,64 @@ class GpuSliceCodec:
         return [(r, a, min(a + (64 << 20), (c0 + c) * U))
                 for r in range(rows) for a in range(c0 * U, (c0 + c) * U, 64 << 20)]
 
+    def _meta(self, lay, tensors) -> dict:
+        return {"k": self.k, "m": self.m, "unit_bytes": self.unit_bytes,
+                "n_stripes": lay.n_stripes, "n_units": lay.n_units,
+                "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
+
+    def _to_host(self, rows: int, chunks, C: int, src, out: np.ndarray, copy, pool,
+                 produce=None) -> None:
+        """Move chunk n = (first stripe, stripes) of a device (rows, stripes,
+        unit_bytes) source into the host array ``out`` (rows, S * unit_bytes)
+        through two pinned (rows, C, unit_bytes) buffers: transfers on the
+        ``copy`` stream, row by row (a row's part of a chunk is contiguous),
+        then 64 MiB pieces copied out by the thread pool while the next chunk
+        is in flight.  ``src(n)`` is chunk n's device view; ``produce(n,
+        landed)``, when given, enqueues what fills it and makes ``copy`` wait
+        for that (``landed[j]`` = chunk j has reached pinned memory)."""
+        U, nb = self.unit_bytes, min(2, len(chunks))
+        pins = [torch.empty((rows, C, U), dtype=torch.uint8, pin_memory=True)
+                for _ in range(nb)]
+        landed: List[torch.cuda.Event] = []
+        drained: List[list] = []   # host copies of chunk n out of pins[n % nb]
+
+        def drain(n):
+            c0, c = chunks[n]
+            flat = pins[n % nb].numpy().reshape(rows, -1)
+            landed[n].synchronize()
+            return [pool.submit(np.copyto, out[r, a:b], flat[r, a - c0 * U:b - c0 * U])
+                    for r, a, b in self._pieces(rows, c0, c, U)]
+
+        for n, (c0, c) in enumerate(chunks):
+            b = n % nb
+            if produce is not None:
+                produce(n, landed)
+            if n >= nb:
+                for f in drained[n - nb]:   # pinned buffer b is free again
+                    f.result()
+            view = src(n)
+            with torch.cuda.stream(copy):
+                for r in range(rows):
+                    pins[b][r, :c].copy_(view[r], non_blocking=True)
+            landed.append(torch.cuda.Event())
+            landed[-1].record(copy)
+            if n >= 1:
+                drained.append(drain(n - 1))   # overlaps chunk n's transfer
+        drained.append(drain(len(chunks) - 1))
+        for fs in drained[-nb:]:
+            for f in fs:
+                f.result()
+
+    def _pool(self) -> ThreadPoolExecutor:
+        return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
+
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
+        """Code and stage in bounded chunks; returns when the slices are in
+        host memory.  The kernels run on torch's current stream (ordered after
+        the work that produced the tensors), the transfers on the device's
+        side stream."""
         from . import _lib
-        from .codec import stream_handle
+        from .codec import side_stream, stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
         lay = self._layout.StripeLayout(tensors, k, m, U)
@@ -186,28 +287,19 @@ class GpuSliceCodec:
         nb = min(2, len(chunks))
         out = self._host_out((k + m, S * U))
         one = np.ones((1, 1), np.uint8)
-        with torch.cuda.device(dev), \
-                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
-            comp, copy = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
+        with torch.cuda.device(dev), self._pool() as pool:
+            comp, copy = torch.cuda.current_stream(dev), side_stream(dev)
             bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
-            pins = [torch.empty((k + m, C, U), dtype=torch.uint8, pin_memory=True)
-                    for _ in range(nb)]
             # per buffer: parity unit (s, i) -> row k + i, data unit (s, p) -> row p
             pp = [self._dev(np.stack([self._rows(b, k + i) for i in range(m)], axis=1), np.int64,
                             dev) for b in bufs]
             gp = [self._dev(np.stack([self._rows(b, p) for p in range(k)], axis=1), np.int64, dev)
                   for b in bufs]
-            landed: List[torch.cuda.Event] = []   # chunk n is in pins[n % nb]
-            drained: List[list] = []              # host copies of chunk n out of pins
+            for b in bufs:
+                b.record_stream(copy)
 
-            def drain(n):
+            def produce(n, landed):
                 c0, c = chunks[n]
-                flat = pins[n % nb].numpy().reshape(k + m, -1)
-                landed[n].synchronize()
-                return [pool.submit(np.copyto, out[r, a:b], flat[r, a - c0 * U:b - c0 * U])
-                        for r, a, b in self._pieces(k + m, c0, c, U)]
-
-            for n, (c0, c) in enumerate(chunks):
                 b = n % nb
                 if n >= nb:
                     comp.wait_event(landed[n - nb])    # device buffer b is free again
@@ -221,28 +313,71 @@ class GpuSliceCodec:
                     stream_handle(comp, dev)), "ec_encode_batched (gather)")
                 ready = torch.cuda.Event()
                 ready.record(comp)
-                if n >= nb:
-                    for f in drained[n - nb]:           # pinned buffer b is free again
-                        f.result()
                 copy.wait_event(ready)
-                with torch.cuda.stream(copy):  # row by row: each row's part is contiguous
-                    for r in range(k + m):
-                        pins[b][r, :c].copy_(bufs[b][r, :c], non_blocking=True)
-                landed.append(torch.cuda.Event())
-                landed[-1].record(copy)
-                if n >= 1:
-                    drained.append(drain(n - 1))      # overlaps chunk n's transfer
-            drained.append(drain(len(chunks) - 1))
-            for fs in drained[-nb:]:
-                for f in fs:
-                    f.result()
-        meta = {"k": k, "m": m, "unit_bytes": U, "n_stripes": S, "n_units": lay.n_units,
-                "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
-        return meta, [out[p] for p in range(k + m)]
+
+            self._to_host(k + m, chunks, C, lambda n: bufs[n % nb][:, :chunks[n][1]], out,
+                          copy, pool, produce)
+        return self._meta(lay, tensors), [out[p] for p in range(k + m)]
+
+    def snapshot(self, tensors: Sequence[torch.Tensor], hold: bool = True) -> "PendingSlices":
+        """Code the tensors into one (k + m, stripes, unit_bytes) block in HBM
+        and stage it to host memory in the background.
+
+        The parity launch and the gather launch run on the device's side
+        stream (its own hardware queue) after the work already enqueued on
+        torch's current stream; with ``hold`` the current stream then waits
+        for them, so later work there (the next optimizer step) cannot change
+        the tensors before they are coded.  That wait is the whole stall of a
+        save: the block is (k + m) / k of the state in HBM, written at HBM
+        speed.  A background thread moves the block to host memory as
+        ``encode`` does and frees it; ``PendingSlices.result()`` returns
+        ``(meta, slices)`` as ``encode`` would.  Without ``hold`` the caller
+        must order its own writes after ``PendingSlices.coded``."""
+        from . import _lib
+        from .codec import side_stream, stream_handle
+        k, m, U = self.k, self.m, self.unit_bytes
+        tensors = list(tensors)
+        lay = self._layout.StripeLayout(tensors, k, m, U)
+        S, dev = lay.n_stripes, lay.device
+        side = side_stream(dev)
+        cur = torch.cuda.current_stream(dev)
+        with torch.cuda.device(dev):
+            block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
+            pp = self._dev(np.stack([self._rows(block, k + i) for i in range(m)], axis=1),
+                           np.int64, dev)
+            gp = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1),
+                           np.int64, dev)
+        for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
+            t.record_stream(side)
+        side.wait_stream(cur)   # the tensors' producers and the descriptor uploads
+        _lib.check(_lib.lib().ec_encode_batched(
+            _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+            pp.data_ptr(), S, U, stream_handle(side, dev)), "ec_encode_batched")
+        _lib.check(_lib.lib().ec_encode_batched(
+            _lib.u8ptr(np.ones((1, 1), np.uint8)), 1, 1, lay.d_ptrs.data_ptr(),
+            lay.d_len.data_ptr(), gp.data_ptr(), S * k, U, stream_handle(side, dev)),
+            "ec_encode_batched (gather)")
+        coded = torch.cuda.Event()
+        coded.record(side)
+        if hold:
+            cur.wait_event(coded)
+        C = self._chunk_stripes(S, k + m)
+        chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
+
+        def stage():
+            nonlocal block
+            out = self._host_out((k + m, S * U))
+            with torch.cuda.device(dev), self._pool() as pool:
+                self._to_host(k + m, chunks, C, lambda n: block[:, chunks[n][0]:sum(chunks[n])],
+                              out, side, pool)
+            block = None   # back to the allocator: the last transfer has landed
+            return [out[p] for p in range(k + m)]
+
+        return PendingSlices(self._meta(lay, tensors), coded, stage)
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib
-        from .codec import decode_matrix, stream_handle
+        from .codec import decode_matrix, side_stream, stream_handle
         k, m, U, S = meta["k"], meta["m"], meta["unit_bytes"], meta["n_stripes"]
         if len(slices) < k:
             raise CheckpointingException(f"only {len(slices)} of the {k} slices needed")
@@ -269,10 +404,11 @@ class GpuSliceCodec:
         nb = min(2, len(chunks))
         one = np.ones((1, 1), np.uint8)
         hp = [p for _, p in have]
-        with torch.cuda.device(device), \
-                ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
-            comp, copy = torch.cuda.current_stream(device), torch.cuda.Stream(device)
+        with torch.cuda.device(device), self._pool() as pool:
+            comp, copy = torch.cuda.current_stream(device), side_stream(device)
             bufs = [torch.empty((k, C, U), dtype=torch.uint8, device=device) for _ in range(nb)]
+            for bf in bufs:
+                bf.record_stream(copy)
             pins = [torch.empty((k, C, U), dtype=torch.uint8, pin_memory=True)
                     for _ in range(nb)]
             # Every descriptor array is uploaded once, stripe-major, so that a

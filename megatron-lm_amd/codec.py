@@ -12,7 +12,8 @@ used by ``manager.save`` at megatron/training/checkpointing.py:538-541 and
 from __future__ import annotations
 
 import ctypes
-from typing import List, Optional, Sequence
+import threading
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -47,6 +48,34 @@ def stream_handle(stream: Optional[torch.cuda.Stream] = None,
         if device is not None and s.device != torch.device(device):
             raise ValueError(f"stream is on {s.device}, the tensors on {device}")
     return ctypes.c_void_p(s.cuda_stream)
+
+
+_side: Dict[Tuple[int, int], torch.cuda.ExternalStream] = {}
+_side_lock = threading.Lock()
+
+
+def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
+    """A stream of ``device`` with a hardware queue of its own
+    (``ec_stream_create``), for checkpoint work that should run beside the
+    training stream rather than behind it: torch's pooled streams share a few
+    hardware queues with the current stream, and work on one queue runs in
+    order.  ``cus`` > 0 restricts it to the first ``cus`` CUs.  One stream per
+    (device, cus), created on first use and kept for the life of the process
+    (the runtime hands out few such queues)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None \
+        else torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError(f"side_stream needs a HIP device, got {dev}")
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, max(0, int(cus)))
+    with _side_lock:
+        s = _side.get(key)
+        if s is None:
+            h = ctypes.c_void_p()
+            _lib.check(_lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h)),
+                       "ec_stream_create")
+            s = _side[key] = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
+        return s
 
 
 # ------------------------------------------------------------ host algebra --

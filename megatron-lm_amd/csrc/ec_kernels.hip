@@ -31,11 +31,13 @@
 // running parity are combined with v_bitop3_b32 (XOR3), so one coefficient
 // costs 3 permutes + 1.5 XOR3 per dword, and the field selectors (5 ops per
 // dword) are shared by all m outputs.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <array>
 #include <utility>
+#include <vector>
 
 #include "ec_mi355.h"
 #include "gf256.h"
@@ -1411,6 +1413,39 @@ int ec_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* d_new_p
                                       nullptr, n_stripes, unit_bytes, true, st);
   return ec::kUpdTable[k - 1][m - 1](coeff, d_new_ptrs, d_old_ptrs, d_len, d_parity_ptrs,
                                      n_stripes, unit_bytes, st);
+}
+
+int ec_stream_create(int device, int n_cus, ec_stream_t* out) {
+  if (!out) return EC_EINVAL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return EC_EHIP;
+  if (device < 0 || device >= count) return EC_EINVAL;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    return EC_EHIP;
+  const int n = (n_cus <= 0 || n_cus > cus) ? cus : n_cus;
+  std::vector<uint32_t> mask((cus + 31) / 32, 0u);
+  for (int c = 0; c < n; ++c) mask[c / 32] |= 1u << (c % 32);
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
+  if (prev != device && hipSetDevice(device) != hipSuccess) return EC_EHIP;
+  hipStream_t st = nullptr;
+  const hipError_t e =
+      hipExtStreamCreateWithCUMask(&st, static_cast<uint32_t>(mask.size()), mask.data());
+  if (prev != device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return EC_EHIP;
+  }
+  *out = st;
+  return EC_OK;
+}
+
+int ec_stream_destroy(ec_stream_t stream) {
+  if (!stream) return EC_EINVAL;
+  return hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)) == hipSuccess ? EC_OK : EC_EHIP;
 }
 
 }  // extern "C"

@@ -84,3 +84,70 @@ def test_gpu_encode_reuses_host_array_only_when_free(pkg, dev):
     assert meta3 == meta2 and all(np.array_equal(a, b) for a, b in zip(third, want))
     _, oracle_slices = OracleSliceCodec(4, 2, 1024).encode([t.cpu() for t in gpu2])
     assert all(np.array_equal(a, b) for a, b in zip(third, oracle_slices))
+
+
+def _bump(t):
+    """Change every element in place, on torch's current stream."""
+    return t.add_(1) if t.is_floating_point() else t.bitwise_xor_(1)
+
+
+@pytest.mark.parametrize("k,m,unit,chunk_stripes", [(4, 2, 1024, None), (6, 3, 4096, 2),
+                                                    (12, 4, 65536, None), (3, 2, 256, 1)])
+def test_gpu_snapshot_codes_the_state_at_the_call(pkg, dev, k, m, unit, chunk_stripes):
+    """snapshot() codes the tensors as they are when it is called: writes
+    enqueued on torch's stream right after it (the next optimizer step) do not
+    reach the slices, which equal the oracle's byte for byte, and decode."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    kw = {} if chunk_stripes is None else {"chunk_bytes": chunk_stripes * (k + m) * unit}
+    cpu = make_tensors(1) + make_tensors(3)
+    gpu = [t.to(dev) for t in cpu]
+    codec = GpuSliceCodec(k, m, unit, **kw)
+    pending = codec.snapshot(gpu)
+    for t in gpu:
+        _bump(t)
+    meta, slices = pending.result(timeout=120)
+    assert pending.done()
+    ometa, oslices = OracleSliceCodec(k, m, unit).encode(cpu)
+    assert meta == ometa
+    for p, (a, b) in enumerate(zip(slices, oslices)):
+        assert np.array_equal(a, b), f"slice {p}"
+    keep = list(range(m, k + m))   # the first m data slices lost
+    out = codec.decode(meta, {p: slices[p] for p in keep}, dev)
+    assert same(out, cpu)
+
+
+def test_gpu_snapshots_in_flight_together(pkg, dev):
+    """Two snapshots staged at once (one codec, different states) both come
+    back whole, and a synchronous encode between them is unaffected."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    codec = GpuSliceCodec(4, 2, 2048, chunk_bytes=3 * 6 * 2048)
+    a_cpu, b_cpu = make_tensors(2), make_tensors(3)
+    a, b = [t.to(dev) for t in a_cpu], [t.to(dev) for t in b_cpu]
+    pa = codec.snapshot(a)
+    pb = codec.snapshot(b)
+    _, mid = codec.encode(a)
+    _, sa = pa.result(timeout=120)
+    _, sb = pb.result(timeout=120)
+    oracle = OracleSliceCodec(4, 2, 2048)
+    for got, ref in ((sa, oracle.encode(a_cpu)[1]), (sb, oracle.encode(b_cpu)[1]),
+                     (mid, oracle.encode(a_cpu)[1])):
+        assert all(np.array_equal(x, y) for x, y in zip(got, ref))
+
+
+def test_gpu_side_stream(pkg, dev):
+    """ec_stream_create: one cached stream per (device, CUs); the encode on it
+    matches the one on torch's stream, also restricted to 64 CUs."""
+    s_all = pkg.side_stream(dev)
+    assert pkg.side_stream(dev) is s_all and s_all.device == dev
+    s_64 = pkg.side_stream(dev, cus=64)
+    assert s_64 is not s_all
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    data = [torch.randint(0, 256, (1 << 20,), dtype=torch.uint8, device=dev, generator=g)
+            for _ in range(6)]
+    ref = pkg.rs_encode(data, 3)
+    for s in (s_all, s_64):
+        s.wait_stream(torch.cuda.current_stream(dev))
+        out = pkg.rs_encode(data, 3, stream=s)
+        s.synchronize()
+        assert all(torch.equal(x, y) for x, y in zip(out, ref))
