@@ -11,8 +11,9 @@ megatron/training/training.py:806-838).
 This module fills the reserved choice:
 
 * ``add_erasure_coding_args(parser)`` adds ``--ec-data-units`` (k),
-  ``--ec-parity-units`` (m), ``--ec-unit-bytes`` and ``--ec-jump`` to a parser, and the
-  reference's own checkpoint flags when the parser lacks them;
+  ``--ec-parity-units`` (m), ``--ec-unit-bytes``, ``--ec-jump`` and
+  ``--[no-]ec-stage-in-background`` to a parser, and the reference's own
+  checkpoint flags when the parser lacks them;
 * ``validate_erasure_coding_args(args)`` applies the reference's rules to
   ``in_memory`` (a local directory is required, as for ``local``) and checks
   the code's shape;
@@ -65,6 +66,11 @@ def add_erasure_coding_args(parser: argparse.ArgumentParser) -> argparse.Argumen
                             "their local checkpoint.")
     group.add_argument("--ec-unit-bytes", type=int, default=4 << 20,
                        help="Bytes per coded unit (a multiple of 16).")
+    group.add_argument("--ec-stage-in-background", action=argparse.BooleanOptionalAction,
+                       default=True,
+                       help="Asynchronous saves (--async-save) code the state into GPU memory, "
+                            "hold training only for that, and stage, exchange and write the "
+                            "slices from a background thread.")
     group.add_argument("--ec-jump", type=int, default=None,
                        help="Spacing J between the ranks holding one rank's k + m slices "
                             "(rank n, n + J, n + 2J, ...), as --replication-jump; set it to "
@@ -106,4 +112,5 @@ def build_checkpointing_context(args, group=None, codec=None) -> dict:
                                     args.ec_unit_bytes, group=group, codec=codec,
                                     jump=args.ec_jump or 1)
     return {"local_checkpoint_manager":
-            ECLocalCheckpointManager(args.non_persistent_local_ckpt_dir, strategy)}
+            ECLocalCheckpointManager(args.non_persistent_local_ckpt_dir, strategy,
+                                     stage_in_background=args.ec_stage_in_background)}

@@ -52,6 +52,7 @@ import os
 import re
 import sys
 import threading
+import time
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -512,24 +513,26 @@ class ErasureCodedStrategy:
                 f"{self.k + self.m} distinct slices")
 
     def _exchange(self, outgoing: Dict[Tuple[int, int, int], np.ndarray],
-                  incoming: List[Tuple[int, int, int, int]]) -> Dict[Tuple[int, int, int], np.ndarray]:
+                  incoming: List[Tuple[int, int, int, int]],
+                  group: Optional[dist.ProcessGroup] = None) -> Dict[Tuple[int, int, int], np.ndarray]:
         """Point-to-point exchange.  outgoing[(dst, owner, pos)] = bytes to send;
         incoming = [(src, owner, pos, nbytes)] to receive.  Every rank passes
         the lists the plan gives it; transfers are ordered by (owner, pos) so
         that both sides agree on tags."""
         me = dist.get_rank()
+        group = self.group if group is None else group
         reqs, recv = [], {}
         for (src, owner, pos, n) in sorted(incoming, key=lambda x: (x[1], x[2])):
             if src == me:
                 continue
             buf = torch.empty(n, dtype=torch.uint8)
             recv[(src, owner, pos)] = buf
-            reqs.append(dist.irecv(buf, src=src, group=self.group, tag=owner * 4096 + pos))
+            reqs.append(dist.irecv(buf, src=src, group=group, tag=owner * 4096 + pos))
         for (dst, owner, pos), data in sorted(outgoing.items(), key=lambda x: (x[0][1], x[0][2])):
             if dst == me:
                 continue
             reqs.append(dist.isend(torch.from_numpy(np.ascontiguousarray(data)), dst=dst,
-                                   group=self.group, tag=owner * 4096 + pos))
+                                   group=group, tag=owner * 4096 + pos))
         for r in reqs:
             r.wait()
         return {key: v.numpy() for key, v in recv.items()}
@@ -589,11 +592,15 @@ class ECLocalCheckpointManager:
     redundancy, called like the reference's LocalCheckpointManager:
     ``save(state, iteration, is_async)``, ``find_latest()``, ``load()``."""
 
-    def __init__(self, root_dir, repl_strategy: ErasureCodedStrategy):
+    def __init__(self, root_dir, repl_strategy: ErasureCodedStrategy,
+                 stage_in_background: bool = False):
         self.root = Path(root_dir)
         self.strategy = repl_strategy
         self.rank = dist.get_rank()
         self.latest_iteration = -1
+        self.stage_in_background = stage_in_background
+        self._bg_group = None
+        self._bg_last: Optional[threading.Thread] = None
 
     # paths
     @property
@@ -651,55 +658,35 @@ class ECLocalCheckpointManager:
         Its ``async_fn`` is a module-level function of picklable arguments, so
         either async caller (forked or persistent) can run it; its finalize
         function checks the files and agrees on success across the group.
-        ``execute_sync()`` runs it all in place."""
+        ``execute_sync()`` runs it all in place.
+
+        With is_async on a manager built with ``stage_in_background``, only
+        the coding runs here (``codec.snapshot``: torch's stream waits for it,
+        after which the tensors may change); staging to host memory, the
+        exchange (over a gloo group of its own) and the writes run in a
+        background thread of this process, and the request's ``async_fn``
+        waits for that thread's marker file."""
         st = self.strategy
         st.check_group()
-        me = self.rank
-        error = None
-        received: Dict[Tuple[int, int, int], np.ndarray] = {}
+        if is_async and self.stage_in_background:
+            return self._save_in_background(state, iteration)
+        error, blobs = None, None
         try:
             # .tensors of MCoreTensorAwareStateDict is an iterator: take it once
             tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
-            hollow = _hollow_state(state)
-            common = state.common if isinstance(state, TensorListState) else {}
+            hollow, common = _hollow_state(state), _common(state)
             meta, slices = st.codec.encode(tensors)
-            meta["common"] = common
-            meta["owner"] = me
-            meta["iteration"] = iteration
-            blobs = {p: _pack({**meta, "pos": p}, s, hollow) for p, s in enumerate(slices)}
-            sizes = torch.tensor([blobs[p].size for p in range(st.k + st.m)], dtype=torch.int64)
+            blobs = self._blobs(meta, slices, hollow, common, iteration)
         except Exception as e:  # noqa: BLE001 - reported collectively below
             error = e
-            sizes = torch.full((st.k + st.m,), -1, dtype=torch.int64)
-        # every rank learns every blob size (and who failed)
-        ranks = st.ranks()
-        all_sizes = [torch.empty_like(sizes) for _ in ranks]
-        dist.all_gather(all_sizes, sizes, group=st.group)
-        failed = any(int(s[0]) < 0 for s in all_sizes)
-        if not failed:
-            outgoing = {(st.holder(me, p), me, p): blobs[p] for p in range(st.k + st.m)}
-            incoming = []
-            for owner, sz in zip(ranks, all_sizes):
-                for p in range(st.k + st.m):
-                    if st.holder(owner, p) == me:
-                        incoming.append((owner, owner, p, int(sz[p])))
-            got = st._exchange(outgoing, incoming)
-            for (src, owner, p), buf in got.items():
-                received[(owner, p)] = buf
-            for p in range(st.k + st.m):
-                if st.holder(me, p) == me:
-                    received[(me, p)] = blobs[p]
-
-        if failed:
+        received = self._place(blobs, st.group)
+        if received is None:
             raise CheckpointingException(
                 f"erasure-coded save of iteration {iteration} failed on some rank") from error
-        jobs = [(str(self._slice_path(iteration, owner, p)), torch.from_numpy(blob))
-                for (owner, p), blob in sorted(received.items())]
-        expected = [(path, int(t.numel())) for path, t in jobs]
+        jobs, expected = self._jobs(iteration, received)
 
         def finalize():
-            ok = all(os.path.isfile(path) and os.path.getsize(path) == n for path, n in expected)
-            self._finish_save(iteration, ok)
+            self._finish_save(iteration, _files_complete(expected))
 
         self.local_dir.mkdir(parents=True, exist_ok=True)
         if is_async:
@@ -710,6 +697,101 @@ class ECLocalCheckpointManager:
             pass  # finalize() sees the missing files and fails the save everywhere
         finalize()
         return None
+
+    def _blobs(self, meta: dict, slices, hollow: bytes, common: dict,
+               iteration: int) -> Dict[int, np.ndarray]:
+        meta = {**meta, "common": common, "owner": self.rank, "iteration": iteration}
+        return {p: _pack({**meta, "pos": p}, sl, hollow) for p, sl in enumerate(slices)}
+
+    def _place(self, blobs: Optional[Dict[int, np.ndarray]],
+               group) -> Optional[Dict[Tuple[int, int], np.ndarray]]:
+        """Every rank's blob sizes to every rank (-1: that rank failed), then,
+        if none failed, the exchange: {(owner, pos): blob} this rank holds.
+        None on every rank if any rank failed.  Collective over ``group``."""
+        st, me = self.strategy, self.rank
+        n = st.k + st.m
+        sizes = torch.full((n,), -1, dtype=torch.int64) if blobs is None else \
+            torch.tensor([blobs[p].size for p in range(n)], dtype=torch.int64)
+        ranks = st.ranks()
+        all_sizes = [torch.empty_like(sizes) for _ in ranks]
+        dist.all_gather(all_sizes, sizes, group=group)
+        if any(int(sz[0]) < 0 for sz in all_sizes):
+            return None
+        outgoing = {(st.holder(me, p), me, p): blobs[p] for p in range(n)}
+        incoming = [(owner, owner, p, int(sz[p])) for owner, sz in zip(ranks, all_sizes)
+                    for p in range(n) if st.holder(owner, p) == me]
+        received = {(owner, p): buf for (_, owner, p), buf in
+                    st._exchange(outgoing, incoming, group).items()}
+        for p in range(n):
+            if st.holder(me, p) == me:
+                received[(me, p)] = blobs[p]
+        return received
+
+    def _jobs(self, iteration: int, received):
+        jobs = [(str(self._slice_path(iteration, owner, p)), torch.from_numpy(blob))
+                for (owner, p), blob in sorted(received.items())]
+        return jobs, [(path, int(t.numel())) for path, t in jobs]
+
+    def _background_group(self):
+        """A gloo group over the strategy's ranks for the background thread's
+        collectives, so they never interleave with the caller's on the
+        strategy's group.  Created by the members only."""
+        if self._bg_group is None:
+            self._bg_group = dist.new_group(ranks=self.strategy.ranks(), backend="gloo",
+                                            use_local_synchronization=True)
+        return self._bg_group
+
+    def _save_in_background(self, state, iteration: int) -> "AsyncSaveRequest":
+        st = self.strategy
+        error, pending, hollow, common = None, None, b"", {}
+        try:
+            tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
+            hollow, common = _hollow_state(state), _common(state)
+            pending = st.codec.snapshot(tensors)
+        except Exception as e:  # noqa: BLE001 - reported collectively by the thread
+            error = e
+        group = self._background_group()
+        self.local_dir.mkdir(parents=True, exist_ok=True)
+        marker = self.local_dir / f".iter_{iteration:07d}.staged"
+        marker.unlink(missing_ok=True)
+        prev, box = self._bg_last, {"ok": False, "expected": []}
+
+        def body():
+            try:
+                if prev is not None:
+                    prev.join()   # one save's collectives at a time, in save order
+                blobs = None
+                try:
+                    if error is not None:
+                        raise error
+                    meta, slices = pending.result()
+                    blobs = self._blobs(meta, slices, hollow, common, iteration)
+                    del slices
+                except Exception as e:  # noqa: BLE001 - reported collectively
+                    box["error"] = e
+                received = self._place(blobs, group)
+                if received is not None:
+                    jobs, box["expected"] = self._jobs(iteration, received)
+                    del received, blobs
+                    _write_slice_files(jobs)
+                    box["ok"] = True
+            except Exception as e:  # noqa: BLE001 - finalize fails the save everywhere
+                box.setdefault("error", e)
+            finally:
+                tmp = marker.with_name(marker.name + ".tmp")
+                tmp.write_text("ok" if box["ok"] else "failed")
+                os.replace(tmp, marker)
+
+        thread = threading.Thread(target=body, daemon=True, name=f"ec-save-{iteration}")
+        thread.start()
+        self._bg_last = thread
+
+        def finalize():
+            thread.join()
+            marker.unlink(missing_ok=True)
+            self._finish_save(iteration, box["ok"] and _files_complete(box["expected"]))
+
+        return AsyncSaveRequest(_await_marker, (str(marker),), [finalize])
 
     def _finish_save(self, iteration: int, ok: bool) -> None:
         flag = torch.tensor([0 if ok else 1], dtype=torch.int64)
@@ -806,6 +888,27 @@ class ECLocalCheckpointManager:
             state.insert_tensors(tensors)
             return state, self._ckpt_id(it)
         return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
+
+
+def _common(state) -> dict:
+    return state.common if isinstance(state, TensorListState) else {}
+
+
+def _files_complete(expected: Sequence[Tuple[str, int]]) -> bool:
+    return all(os.path.isfile(path) and os.path.getsize(path) == n for path, n in expected)
+
+
+def _await_marker(path: str, timeout: float = 3600.0) -> None:
+    """``async_fn`` of a save staged in the background: returns once the
+    trainer's background thread has finished this rank's part and written its
+    marker file (whether it succeeded is the finalize function's business).
+    No GPU work; module-level with picklable arguments, so it can run in a
+    forked or a spawned writer."""
+    end = time.monotonic() + timeout
+    while not os.path.exists(path):
+        if time.monotonic() > end:
+            raise TimeoutError(f"{path} did not appear within {timeout} s")
+        time.sleep(0.01)
 
 
 def _write_slice_files(jobs: Sequence[Tuple[str, torch.Tensor]]) -> None:

@@ -23,6 +23,11 @@ def make_tensors(rank, device="cpu"):
     return out
 
 
+def bump(t):
+    """Change every element in place (an optimizer step)."""
+    return t.add_(1) if t.is_floating_point() else t.bitwise_xor_(1)
+
+
 def same(a, b):
     return len(a) == len(b) and all(
         x.dtype == y.dtype and x.shape == y.shape and
@@ -50,7 +55,8 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             from ec_cpu_codec import OracleSliceCodec
             codec = OracleSliceCodec(k, m, unit)
         strat = ErasureCodedStrategy(k, m, unit, codec=codec, jump=jump)
-        mgr = ECLocalCheckpointManager(root, strat)
+        mgr = ECLocalCheckpointManager(root, strat,
+                                       stage_in_background=scenario.startswith("background"))
         mine = make_tensors(rank, device)
         state = TensorListState([t.clone() for t in mine], {"rank": rank})
 
@@ -205,6 +211,67 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             assert not any(n.startswith("iter_0000003") for n in names), names
             got, name = mgr.load()
             assert name == f"iter_0000004_{rank}_local" and same(got.tensors, mine)
+        elif scenario == "background":
+            # A save staged in the background: save() returns once the state
+            # is coded, the next optimizer step changes the tensors at once,
+            # and the checkpoint still holds the state of the call.  The
+            # request goes through the reference queue's steps (freeze, ship
+            # without finalize functions to a writer, finalize on every rank).
+            import pickle
+            mgr.save(state, 1)
+            req = mgr.save(state, 2, is_async=True)
+            for t in state.tensors:
+                bump(t)
+            frozen = req.freeze()
+            ship = frozen._replace(call_idx=1, finalize_fns=[])
+            pickle.dumps(ship)
+            if use_gpu:   # no fork of a process that holds the GPU
+                ship.async_fn(*ship.async_fn_args, **ship.async_fn_kwargs)
+            else:
+                proc = torch.multiprocessing.get_context("fork").Process(
+                    target=ship.async_fn, args=ship.async_fn_args, kwargs=ship.async_fn_kwargs)
+                proc.start()
+                proc.join()
+                assert proc.exitcode == 0
+            dist.barrier()
+            for fn in frozen.finalize_fns:
+                fn()
+            assert mgr.latest_iteration == 2
+            names = {f.name for f in mgr.local_dir.iterdir()}
+            assert not any(n.startswith("iter_0000001") or n.startswith(".") for n in names), names
+            got, name = mgr.load()
+            assert name == f"iter_0000002_{rank}_local" and same(got.tensors, mine)
+            # two saves in flight before either is finalized
+            bumped = [t.clone() for t in state.tensors]
+            r3 = mgr.save(state, 3, is_async=True)
+            r4 = mgr.save(state, 4, is_async=True)
+            r3.execute_sync()
+            r4.execute_sync()
+            assert mgr.latest_iteration == 4
+            got, name = mgr.load()
+            assert name == f"iter_0000004_{rank}_local" and same(got.tensors, bumped)
+        elif scenario == "background_fail":
+            # One rank fails before (fail) or during (fail_late) the
+            # background staging: every rank's finalize raises, nothing of
+            # that iteration is left, the previous one stays; then a good save.
+            from ec_cpu_codec import OracleSliceCodec
+            mgr.save(state, 1)
+            for it, kw in ((2, {"fail": True}), (3, {"fail_late": True})):
+                if rank == 1:
+                    strat.codec = OracleSliceCodec(k, m, unit, **kw)
+                req = mgr.save(state, it, is_async=True)
+                try:
+                    req.execute_sync()
+                    raise AssertionError(f"background save with {kw} did not fail")
+                except CheckpointingException:
+                    pass
+                names = {f.name for f in mgr.local_dir.iterdir()}
+                assert not any(n.startswith(f"iter_{it:07d}") or n.startswith(".")
+                               for n in names), names
+                assert mgr.find_latest() == 1
+                strat.codec = OracleSliceCodec(k, m, unit)
+            mgr.save(state, 4, is_async=True).execute_sync()
+            assert mgr.find_latest() == 4
         else:
             raise ValueError(scenario)
         dist.barrier()

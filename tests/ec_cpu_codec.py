@@ -15,9 +15,34 @@ def _tensor_bytes(t):
     return t.detach().contiguous().reshape(-1).view(torch.uint8).numpy()
 
 
+class _Staged:
+    """What GpuSliceCodec.snapshot returns, already complete (or failing
+    when its result is asked for, as a staging error would)."""
+
+    def __init__(self, meta, slices, error=None):
+        self.meta, self._slices, self._error = meta, slices, error
+
+    def done(self):
+        return True
+
+    def result(self, timeout=None):
+        if self._error is not None:
+            raise self._error
+        return self.meta, self._slices
+
+
 class OracleSliceCodec:
-    def __init__(self, k, m, unit_bytes, fail=False):
+    """fail: encode and snapshot raise; fail_late: snapshot returns, its
+    result() raises (a failure during background staging)."""
+
+    def __init__(self, k, m, unit_bytes, fail=False, fail_late=False):
         self.k, self.m, self.unit_bytes, self.fail = k, m, unit_bytes, fail
+        self.fail_late = fail_late
+
+    def snapshot(self, tensors):
+        meta, slices = self.encode(tensors)
+        err = RuntimeError("injected staging failure") if self.fail_late else None
+        return _Staged(meta, slices, err)
 
     def _units(self, bufs):
         U = self.unit_bytes

@@ -77,5 +77,10 @@ def test_build_context(tmp_path):
         assert (st.k, st.m, st.unit_bytes, st.jump) == (2, 1, 4096, 3)
         assert mgr.local_dir == tmp_path / "0"
         assert mgr.find_latest() == -1
+        assert mgr.stage_in_background   # the default
+        off = parse(["--non-persistent-ckpt-type", "in_memory", "--non-persistent-local-ckpt-dir",
+                     str(tmp_path), "--no-ec-stage-in-background"])
+        assert not ec_args.build_checkpointing_context(
+            off, codec=OracleSliceCodec(4, 2, 4 << 20))["local_checkpoint_manager"].stage_in_background
     finally:
         dist.destroy_process_group()

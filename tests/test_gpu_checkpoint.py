@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from ec_cpu_codec import OracleSliceCodec
-from ec_ckpt_worker import make_tensors, same
+from ec_ckpt_worker import bump, make_tensors, same
 from test_checkpoint_cpu import launch
 
 pytestmark = pytest.mark.gpu
@@ -51,6 +51,13 @@ def test_gpu_checkpoint_tensor_aware_state_three_ranks(tmp_path):
     launch(tmp_path, "tasd", world=3, k=2, m=1, unit=2048, use_gpu=True)
 
 
+def test_gpu_checkpoint_background_three_ranks(tmp_path):
+    """Saves staged in the background with the GPU codec's snapshot: the
+    tensors bumped on torch's stream right after save() do not reach the
+    checkpoint; two saves in flight both land."""
+    launch(tmp_path, "background", world=3, k=2, m=1, unit=4096, use_gpu=True)
+
+
 def test_gpu_empty_tensor_list(pkg, dev):
     """A rank with nothing to save still takes part: one all-zero stripe."""
     from megatron_lm_amd.checkpoint import GpuSliceCodec
@@ -86,11 +93,6 @@ def test_gpu_encode_reuses_host_array_only_when_free(pkg, dev):
     assert all(np.array_equal(a, b) for a, b in zip(third, oracle_slices))
 
 
-def _bump(t):
-    """Change every element in place, on torch's current stream."""
-    return t.add_(1) if t.is_floating_point() else t.bitwise_xor_(1)
-
-
 @pytest.mark.parametrize("k,m,unit,chunk_stripes", [(4, 2, 1024, None), (6, 3, 4096, 2),
                                                     (12, 4, 65536, None), (3, 2, 256, 1)])
 def test_gpu_snapshot_codes_the_state_at_the_call(pkg, dev, k, m, unit, chunk_stripes):
@@ -104,7 +106,7 @@ def test_gpu_snapshot_codes_the_state_at_the_call(pkg, dev, k, m, unit, chunk_st
     codec = GpuSliceCodec(k, m, unit, **kw)
     pending = codec.snapshot(gpu)
     for t in gpu:
-        _bump(t)
+        bump(t)
     meta, slices = pending.result(timeout=120)
     assert pending.done()
     ometa, oslices = OracleSliceCodec(k, m, unit).encode(cpu)
