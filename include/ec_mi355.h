@@ -148,6 +148,22 @@ int ec_encode_batched(const uint8_t* coeff, int k, int m,
                       const uint64_t* d_parity_ptrs, uint32_t n_stripes,
                       uint32_t unit_bytes, ec_stream_t stream);
 
+/* ec_encode_batched, and in the same pass a copy of every data unit:
+ * unit (s, j) is written, zero-padded to unit_bytes, at d_copy_ptrs[s*k + j]
+ * (0 = no copy of that unit).  The data is read once for the parity and the
+ * copy, so coding a checkpoint into one contiguous block (the data units as
+ * the block's first k rows, the parity as its last m) costs one pass over
+ * HBM.  Copies must not overlap the inputs or the parity.  Same limits and
+ * alignment rules as ec_encode_batched (16-byte aligned copies take the fast
+ * path); k > 16 or m > 4 runs the encode and the copies as two launches.
+ * Serves manager.save at checkpointing.py:538-541: the snapshot of the
+ * tensors of tensor_aware_state_dict.py:179-184 that training may overwrite
+ * as soon as the call's work has run. */
+int ec_encode_batched_copy(const uint8_t* coeff, int k, int m,
+                           const uint64_t* d_data_ptrs, const uint32_t* d_data_len,
+                           const uint64_t* d_parity_ptrs, const uint64_t* d_copy_ptrs,
+                           uint32_t n_stripes, uint32_t unit_bytes, ec_stream_t stream);
+
 /* Batched reconstruct: the stripes of an ec_encode_batched layout that lost
  * the same e shard positions, recovered in one launch with the rows of
  * ec_decode_matrix (e x k):

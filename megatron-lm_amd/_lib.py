@@ -35,6 +35,7 @@ EXPORTS = (
     "ec_rs_encode",
     "ec_rs_decode",
     "ec_encode_batched",
+    "ec_encode_batched_copy",
     "ec_decode_batched",
     "ec_parity_update",
     "ec_stream_create",
@@ -97,6 +98,8 @@ def lib() -> ctypes.CDLL:
     L.ec_rs_decode.argtypes = [_u8p, _i, _i, _vp, _vp, _u64, _vp]
     L.ec_encode_batched.restype = _i
     L.ec_encode_batched.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _u32, _u32, _vp]
+    L.ec_encode_batched_copy.restype = _i
+    L.ec_encode_batched_copy.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
     L.ec_decode_batched.restype = _i
     L.ec_decode_batched.argtypes = [_u8p, _i, _i, _vp, _vp, _vp, _vp, _u32, _u32, _vp]
     L.ec_parity_update.restype = _i

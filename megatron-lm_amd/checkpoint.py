@@ -164,11 +164,11 @@ class GpuSliceCodec:
     the kernel's page faults and zeroing on first touch, which on a 27 GB
     checkpoint halves the staging rate.
 
-    Encode, per chunk: the parity kernel writes the parity units into the
-    device buffer's parity rows and one k = m = 1 gather launch copies the
-    data units into its data rows; the buffer goes to pinned memory on a copy
-    stream, and a thread pool moves it into the result while the next chunk
-    is coded and transferred.  Decode, per chunk: the thread pool copies the k
+    Encode, per chunk: one launch writes the parity units into the device
+    buffer's parity rows and, in the same pass over the data, the data units
+    (zero-padded) into its data rows; the buffer goes to pinned memory on a
+    copy stream, and a thread pool moves it into the result while the next
+    chunk is coded and transferred.  Decode, per chunk: the thread pool copies the k
     slices' part into pinned memory, the copy stream sends it up, one scatter
     launch puts the data rows into fresh tensors and one decode launch
     rebuilds the lost data positions; the next chunk's host copy overlaps.
@@ -176,7 +176,7 @@ class GpuSliceCodec:
     ``snapshot`` is the save path that keeps training running: it codes the
     whole state into one HBM block (288 GB of HBM per MI355X holds a rank's
     (k + m) / k copy) on a stream with its own hardware queue, holds torch's
-    stream only for those two launches, and stages the block to host memory
+    stream only for that launch, and stages the block to host memory
     in a background thread while training goes on.  Transfers use that side
     stream too, so they never queue behind (or in front of) training work."""
 
@@ -287,7 +287,6 @@ class GpuSliceCodec:
         chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
         nb = min(2, len(chunks))
         out = self._host_out((k + m, S * U))
-        one = np.ones((1, 1), np.uint8)
         with torch.cuda.device(dev), self._pool() as pool:
             comp, copy = torch.cuda.current_stream(dev), side_stream(dev)
             bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
@@ -306,12 +305,9 @@ class GpuSliceCodec:
                     comp.wait_event(landed[n - nb])    # device buffer b is free again
                 dp = lay.d_ptrs.data_ptr() + c0 * k * 8
                 dl = lay.d_len.data_ptr() + c0 * k * 4
-                _lib.check(_lib.lib().ec_encode_batched(
-                    _lib.u8ptr(lay.coeff), k, m, dp, dl, pp[b].data_ptr(), c, U,
-                    stream_handle(comp, dev)), "ec_encode_batched")
-                _lib.check(_lib.lib().ec_encode_batched(
-                    _lib.u8ptr(one), 1, 1, dp, dl, gp[b].data_ptr(), c * k, U,
-                    stream_handle(comp, dev)), "ec_encode_batched (gather)")
+                _lib.check(_lib.lib().ec_encode_batched_copy(
+                    _lib.u8ptr(lay.coeff), k, m, dp, dl, pp[b].data_ptr(), gp[b].data_ptr(), c,
+                    U, stream_handle(comp, dev)), "ec_encode_batched_copy")
                 ready = torch.cuda.Event()
                 ready.record(comp)
                 copy.wait_event(ready)
@@ -324,11 +320,11 @@ class GpuSliceCodec:
         """Code the tensors into one (k + m, stripes, unit_bytes) block in HBM
         and stage it to host memory in the background.
 
-        The parity launch and the gather launch run on the device's side
-        stream (its own hardware queue) after the work already enqueued on
-        torch's current stream; with ``hold`` the current stream then waits
-        for them, so later work there (the next optimizer step) cannot change
-        the tensors before they are coded.  That wait is the whole stall of a
+        One launch (parity plus the copy of every data unit, one read of the
+        data) runs on the device's side stream (its own hardware queue) after
+        the work already enqueued on torch's current stream; with ``hold`` the
+        current stream then waits for it, so later work there (the next
+        optimizer step) cannot change the tensors before they are coded.  That wait is the whole stall of a
         save: the block is (k + m) / k of the state in HBM, written at HBM
         speed.  A background thread moves the block to host memory as
         ``encode`` does and frees it; ``PendingSlices.result()`` returns
@@ -351,13 +347,10 @@ class GpuSliceCodec:
         for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
             t.record_stream(side)
         side.wait_stream(cur)   # the tensors' producers and the descriptor uploads
-        _lib.check(_lib.lib().ec_encode_batched(
+        _lib.check(_lib.lib().ec_encode_batched_copy(
             _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
-            pp.data_ptr(), S, U, stream_handle(side, dev)), "ec_encode_batched")
-        _lib.check(_lib.lib().ec_encode_batched(
-            _lib.u8ptr(np.ones((1, 1), np.uint8)), 1, 1, lay.d_ptrs.data_ptr(),
-            lay.d_len.data_ptr(), gp.data_ptr(), S * k, U, stream_handle(side, dev)),
-            "ec_encode_batched (gather)")
+            pp.data_ptr(), gp.data_ptr(), S, U, stream_handle(side, dev)),
+            "ec_encode_batched_copy")
         coded = torch.cuda.Event()
         coded.record(side)
         if hold:

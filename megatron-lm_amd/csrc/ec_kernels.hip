@@ -564,6 +564,8 @@ struct BatchArgs {
   const uint32_t* dlen;  // [n_stripes][K]
   const uint64_t* pptr;  // [n_stripes][M]
   const uint32_t* olen;  // [n_stripes][M] valid output bytes, or null = whole units
+  const uint64_t* cptr;  // [n_stripes][K] copy of each data unit, zero-padded to
+                         // unit_bytes (0 = no copy); read only when the kernel copies
   PermTab tab[M][K];
   uint32_t unit_bytes;
   uint32_t tiles_per_unit;   // tiles of kBlock*U*16 bytes in a unit
@@ -583,8 +585,13 @@ __device__ __align__(16) uint8_t g_zero_tile[kBlock * 4 * 16] = {0};
 // dst[i] at the tile's first byte of output i.  (A branch around each store
 // for outputs that ended early triples the register count, so such tiles
 // take the edge path instead.)
-template <int K, int M, int U>
+//
+// With COPY, cpy[j] points at the tile's first byte of unit j's copy (null:
+// no copy) and the loaded chunk is stored there too: the data is read once
+// for both the parity and the copy.
+template <int K, int M, int U, bool COPY>
 __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
+                                          uint8_t* const (&cpy)[K],
                                           const PermTab (&tab)[M][K]) {
   static_assert(kBlock * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
   uint4 x[U][K];
@@ -602,6 +609,11 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
 #pragma unroll
     for (int i = 0; i < M; ++i)
       store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    if constexpr (COPY) {
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (cpy[j]) store_stream(cpy[j] + rel, x[u][j]);
+    }
   }
 }
 
@@ -609,9 +621,10 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
 // views into a flat buffer at arbitrary offsets): one chunk per lane at a
 // time, each unit read through load_realign (two aligned loads and a byte
 // shift for a misaligned unit); the outputs are aligned.
-template <int K, int M, int U>
+template <int K, int M, int U, bool COPY>
 __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K],
                                                   uint8_t* const (&dst)[M],
+                                                  uint8_t* const (&cpy)[K],
                                                   const PermTab (&tab)[M][K]) {
   constexpr int V = U >= 2 ? 2 : 1;  // chunks per lane in flight together
 #pragma unroll 1
@@ -631,6 +644,11 @@ __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K]
 #pragma unroll
       for (int i = 0; i < M; ++i)
         store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      if constexpr (COPY) {
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+          if (cpy[j]) store_stream(cpy[j] + rel, x[v][j]);
+      }
     }
   }
 }
@@ -639,7 +657,10 @@ __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K]
 // misaligned output): one unit at a time, descriptors re-read from memory,
 // byte-granular at the ends.  Kept as a rolled loop so that its registers
 // stay below the fast path's (the allocator takes the larger of the two).
-template <int K, int M, int U>
+//
+// With COPY, each unit's chunk (zeros past its valid length) also goes to
+// its copy, over the whole unit_bytes.
+template <int K, int M, int U, bool COPY>
 __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, uint32_t base,
                                           const PermTab (&tab)[M][K]) {
   for (int u = 0; u < U; ++u) {
@@ -651,16 +672,22 @@ __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, 
       const uint8_t* dj = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
       uint32_t lj = dj ? a.dlen[(uint64_t)s * K + j] : 0u;
       lj = lj < a.unit_bytes ? lj : a.unit_bytes;
-      if (off >= lj) continue;
-      const uint4 xj = load_unit(dj, off, lj);
-      Fields f[4];
+      uint4 xj = make_uint4(0u, 0u, 0u, 0u);
+      if (off < lj) {
+        xj = load_unit(dj, off, lj);
+        Fields f[4];
 #pragma unroll
-      for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(xj, dd));
+        for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(xj, dd));
 #pragma unroll
-      for (int i = 0; i < M; ++i) {
-        const PermTab t = tab[i][j];
+        for (int i = 0; i < M; ++i) {
+          const PermTab t = tab[i][j];
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+          for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+        }
+      }
+      if constexpr (COPY) {
+        uint8_t* cj = reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]);
+        if (cj) store_unit(cj, off, xj);
       }
     }
 #pragma unroll
@@ -674,7 +701,7 @@ __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, 
   }
 }
 
-template <int K, int M, int U>
+template <int K, int M, int U, bool COPY>
 __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
@@ -704,6 +731,12 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
     olen[i] = l < a.unit_bytes ? l : a.unit_bytes;
     out_aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
   }
+  uint8_t* c[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    c[j] = COPY ? reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]) : nullptr;
+    out_aligned &= (reinterpret_cast<uintptr_t>(c[j]) & 15u) == 0;
+  }
   constexpr uint32_t kTileBytes = kBlock * U * 16u;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t base = t * (kBlock * U) + threadIdx.x;
@@ -712,11 +745,14 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
     // output does not cover it.
     const uint8_t* src[K];
     uint8_t* dst[M];
+    uint8_t* cpy[K];
     bool edge = !out_aligned;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       src[j] = len[j] >= hi ? d[j] + lo : g_zero_tile;
       edge |= len[j] > lo && len[j] < hi;
+      cpy[j] = c[j] ? c[j] + lo : nullptr;
+      if (COPY) edge |= c[j] && a.unit_bytes < hi;  // a copy always spans the unit
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
@@ -724,11 +760,11 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
       edge |= olen[i] < hi;
     }
     if (edge)
-      tile_edge<K, M, U>(a, s, base, tab);
+      tile_edge<K, M, U, COPY>(a, s, base, tab);
     else if (in_aligned)
-      tile_full<K, M, U>(src, dst, tab);
+      tile_full<K, M, U, COPY>(src, dst, cpy, tab);
     else
-      tile_full_realign<K, M, U>(src, dst, tab);
+      tile_full_realign<K, M, U, COPY>(src, dst, cpy, tab);
   }
 }
 
@@ -1067,15 +1103,16 @@ int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st
   return hip_status();
 }
 
-template <int K, int M, int U>
+template <int K, int M, int U, bool COPY>
 int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
-                     const uint64_t* pptr, const uint32_t* olen, uint32_t n_stripes,
-                     uint32_t unit_bytes, hipStream_t st) {
+                     const uint64_t* pptr, const uint32_t* olen, const uint64_t* cptr,
+                     uint32_t n_stripes, uint32_t unit_bytes, hipStream_t st) {
   BatchArgs<K, M> a;
   a.dptr = dptr;
   a.dlen = dlen;
   a.pptr = pptr;
   a.olen = olen;
+  a.cptr = cptr;
   for (int i = 0; i < M; ++i)
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   const uint32_t unit16 = unit_bytes / 16u;
@@ -1093,7 +1130,8 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
-  hipLaunchKernelGGL((batched_kernel<K, M, U>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  hipLaunchKernelGGL((batched_kernel<K, M, U, COPY>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                     st, a);
   return hip_status();
 }
 
@@ -1107,8 +1145,23 @@ int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* d
                    uint32_t unit_bytes, hipStream_t st) {
   constexpr int U = batched_unroll<K>();
   if (U > 1 && unit_bytes % (kBlock * U * 16u) == 0)
-    return launch_batched_u<K, M, U>(coeff, dptr, dlen, pptr, olen, n_stripes, unit_bytes, st);
-  return launch_batched_u<K, M, 1>(coeff, dptr, dlen, pptr, olen, n_stripes, unit_bytes, st);
+    return launch_batched_u<K, M, U, false>(coeff, dptr, dlen, pptr, olen, nullptr, n_stripes,
+                                            unit_bytes, st);
+  return launch_batched_u<K, M, 1, false>(coeff, dptr, dlen, pptr, olen, nullptr, n_stripes,
+                                          unit_bytes, st);
+}
+
+// Encode plus a zero-padded copy of every data unit (cptr), same tiling.
+template <int K, int M>
+int launch_batched_copy(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
+                        const uint64_t* pptr, const uint64_t* cptr, uint32_t n_stripes,
+                        uint32_t unit_bytes, hipStream_t st) {
+  constexpr int U = batched_unroll<K>();
+  if (U > 1 && unit_bytes % (kBlock * U * 16u) == 0)
+    return launch_batched_u<K, M, U, true>(coeff, dptr, dlen, pptr, nullptr, cptr, n_stripes,
+                                           unit_bytes, st);
+  return launch_batched_u<K, M, 1, true>(coeff, dptr, dlen, pptr, nullptr, cptr, n_stripes,
+                                         unit_bytes, st);
 }
 
 template <int K, int M>
@@ -1209,6 +1262,17 @@ constexpr auto batch_table(std::integer_sequence<int, Ks...>) {
   return std::array<std::array<BatchFn, kFastMaxM>, sizeof...(Ks)>{
       batch_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
 }
+using BatchCopyFn = int (*)(const uint8_t*, const uint64_t*, const uint32_t*, const uint64_t*,
+                            const uint64_t*, uint32_t, uint32_t, hipStream_t);
+template <int K, int... Ms>
+constexpr auto batch_copy_row(std::integer_sequence<int, Ms...>) {
+  return std::array<BatchCopyFn, sizeof...(Ms)>{&launch_batched_copy<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto batch_copy_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<BatchCopyFn, kFastMaxM>, sizeof...(Ks)>{
+      batch_copy_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
 template <int K, int... Ms>
 constexpr auto upd_row(std::integer_sequence<int, Ms...>) {
   return std::array<UpdFn, sizeof...(Ms)>{&launch_update<K, Ms + 1>...};
@@ -1231,6 +1295,7 @@ constexpr auto wide_table(std::integer_sequence<int, Ms...>) {
 
 const auto kRsTable = rs_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kBatchTable = batch_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kBatchCopyTable = batch_copy_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kUpdTable = upd_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kXorTable = xor_table(std::make_integer_sequence<int, kFastMaxK>{});
 const auto kWideTable = wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
@@ -1381,6 +1446,30 @@ int ec_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* d_data
                                       nullptr, n_stripes, unit_bytes, false, st);
   return ec::kBatchTable[k - 1][m - 1](coeff, d_data_ptrs, d_data_len, d_parity_ptrs, nullptr,
                                        n_stripes, unit_bytes, st);
+}
+
+int ec_encode_batched_copy(const uint8_t* coeff, int k, int m, const uint64_t* d_data_ptrs,
+                           const uint32_t* d_data_len, const uint64_t* d_parity_ptrs,
+                           const uint64_t* d_copy_ptrs, uint32_t n_stripes, uint32_t unit_bytes,
+                           ec_stream_t stream) {
+  int s = ec::check_batch(coeff, k, m, d_data_ptrs, d_data_len, d_parity_ptrs, unit_bytes);
+  if (s != EC_OK) return s;
+  if (!d_copy_ptrs) return EC_EINVAL;
+  if (n_stripes == 0) return EC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (ec::fast_shape(k, m))
+    return ec::kBatchCopyTable[k - 1][m - 1](coeff, d_data_ptrs, d_data_len, d_parity_ptrs,
+                                             d_copy_ptrs, n_stripes, unit_bytes, st);
+  // Wide codes: the encode, then the copies as k * n_stripes one-unit
+  // stripes of coefficient 1 (the descriptor arrays read as [n_stripes * k][1]).
+  const uint64_t units = (uint64_t)n_stripes * (uint64_t)k;
+  if (units > 0xffffffffull) return EC_ERANGE;
+  s = ec::kBatchWideTable[m - 1](coeff, k, d_data_ptrs, d_data_len, nullptr, d_parity_ptrs,
+                                 nullptr, n_stripes, unit_bytes, false, st);
+  if (s != EC_OK) return s;
+  const uint8_t one = 1;
+  return ec::kBatchTable[0][0](&one, d_data_ptrs, d_data_len, d_copy_ptrs, nullptr,
+                               (uint32_t)units, unit_bytes, st);
 }
 
 int ec_decode_batched(const uint8_t* rows, int k, int e, const uint64_t* d_surv_ptrs,

@@ -105,6 +105,14 @@ def test_device_entry_points_reject_bad_arguments(pkg):
     assert L.ec_encode_batched(c, 6, 3, one, one, one, 1, 100, None) == pkg._lib.EC_EALIGN
     assert L.ec_encode_batched(c, 33, 3, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
     assert L.ec_encode_batched(c, 6, 17, one, one, one, 1, 64, None) == pkg._lib.EC_ERANGE
+    # the copying encode: copy addresses are required; same limits
+    assert L.ec_encode_batched_copy(c, 6, 3, one, one, one, None, 1, 64, None) == \
+        pkg._lib.EC_EINVAL
+    assert L.ec_encode_batched_copy(c, 33, 3, one, one, one, one, 1, 64, None) == \
+        pkg._lib.EC_ERANGE
+    assert L.ec_encode_batched_copy(c, 6, 3, one, one, one, one, 1, 100, None) == \
+        pkg._lib.EC_EALIGN
+    assert L.ec_encode_batched_copy(c, 6, 3, one, one, one, one, 0, 64, None) == pkg._lib.EC_OK
     assert L.ec_decode_batched(c, 6, 3, one, one, one, None, 1, 64, None) == pkg._lib.EC_EINVAL
     assert L.ec_parity_update(c, 6, 3, one, one, None, one, 1, 64, None) == pkg._lib.EC_EINVAL
 

@@ -466,3 +466,50 @@ def test_batched_wide_codes(pkg, dev, k, m, unit, lost):
     fresh = lay.encode()
     torch.cuda.synchronize()
     assert torch.equal(pset.parity, fresh)
+
+
+@pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 4096, False), (6, 3, 16384, False),
+                                               (8, 2, 16384, True), (5, 1, 256, True),
+                                               (3, 2, 4112, False), (20, 6, 2048, True)])
+def test_encode_batched_copy(pkg, dev, k, m, unit, misalign):
+    """ec_encode_batched_copy: the parity equals the oracle's, and every data
+    unit lands zero-padded at its copy address; units with a 0 copy address
+    are skipped (their bytes keep a canary).  Covers the 16 KiB tiles
+    (k <= 8, unit a multiple of 16 KiB), 4 KiB tiles, units shorter than a
+    tile, realigned inputs, a unit size off the tile grid, and a wide code
+    (two launches)."""
+    from megatron_lm_amd import _lib
+    rng = np.random.default_rng(k * 31 + unit)
+    host, tensors = _ragged_device(rng, dev, 30, 5 * unit, misalign)
+    lay = pkg.StripeLayout(tensors, k, m, unit)
+    S = lay.n_stripes
+    block = torch.full((k + m, S, unit), 0xC3, dtype=torch.uint8, device=dev)
+    base = np.uint64(block.data_ptr())
+    rows = np.arange(S, dtype=np.uint64)[:, None]
+    pp = base + ((np.arange(m, dtype=np.uint64)[None, :] + np.uint64(k)) * np.uint64(S) + rows) \
+        * np.uint64(unit)
+    cp = base + (np.arange(k, dtype=np.uint64)[None, :] * np.uint64(S) + rows) * np.uint64(unit)
+    skip = np.zeros((S, k), bool)
+    skip[::3, 1 % k] = True                 # some units are not copied
+    cp[skip] = 0
+    d_pp = torch.from_numpy(pp.view(np.int64)).to(dev)
+    d_cp = torch.from_numpy(np.ascontiguousarray(cp).view(np.int64)).to(dev)
+    _lib.check(_lib.lib().ec_encode_batched_copy(
+        _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+        d_pp.data_ptr(), d_cp.data_ptr(), S, unit, None), "ec_encode_batched_copy")
+    torch.cuda.synchronize()
+    got = block.cpu().numpy()
+    want_par = _oracle_layout_parity(lay, host, unit)        # [S, m, unit]
+    assert np.array_equal(got[k:].transpose(1, 0, 2), want_par)
+    for s in range(S):
+        for j in range(k):
+            u = s * k + j
+            if skip[s, j]:
+                assert (got[j, s] == 0xC3).all(), (s, j)
+                continue
+            want = np.zeros(unit, np.uint8)
+            if u < lay.n_units:
+                t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+                piece = host[t][i * unit: (i + 1) * unit]
+                want[: piece.size] = piece
+            assert np.array_equal(got[j, s], want), (s, j)
