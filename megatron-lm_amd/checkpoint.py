@@ -505,46 +505,55 @@ class ErasureCodedStrategy:
                 f"group of {g} ranks with jump {self.jump} cannot hold k + m = "
                 f"{self.k + self.m} distinct slices")
 
-    def _exchange(self, outgoing: Dict[Tuple[int, int, int], np.ndarray],
-                  incoming: List[Tuple[int, int, int, int]],
+    def _exchange(self, outgoing: Dict[Tuple[int, int, int], object],
+                  incoming: List[Tuple[int, int, int, object]],
                   group: Optional[dist.ProcessGroup] = None) -> Dict[Tuple[int, int, int], np.ndarray]:
-        """Point-to-point exchange.  outgoing[(dst, owner, pos)] = bytes to send;
-        incoming = [(src, owner, pos, nbytes)] to receive.  Every rank passes
+        """Point-to-point exchange.  outgoing[(dst, owner, pos)] = a byte
+        array, or a tuple of byte arrays sent as one message each (a slice's
+        head and payload, never copied together); incoming = [(src, owner,
+        pos, sizes)], sizes the byte count or the tuple of part sizes, each
+        received as one array with the parts back to back.  Every rank passes
         the lists the plan gives it; transfers are ordered by (owner, pos) so
         that both sides agree on tags."""
         me = dist.get_rank()
         group = self.group if group is None else group
         reqs, recv = [], {}
-        for (src, owner, pos, n) in sorted(incoming, key=lambda x: (x[1], x[2])):
+        for (src, owner, pos, sizes) in sorted(incoming, key=lambda x: (x[1], x[2])):
             if src == me:
                 continue
-            buf = torch.empty(n, dtype=torch.uint8)
+            parts = sizes if isinstance(sizes, tuple) else (sizes,)
+            buf = torch.empty(sum(parts), dtype=torch.uint8)
             recv[(src, owner, pos)] = buf
-            reqs.append(dist.irecv(buf, src=src, group=group, tag=owner * 4096 + pos))
+            off = 0
+            for q, n in enumerate(parts):
+                if n:
+                    reqs.append(dist.irecv(buf[off: off + n], src=src, group=group,
+                                           tag=(owner * 4096 + pos) * 2 + q))
+                off += n
         for (dst, owner, pos), data in sorted(outgoing.items(), key=lambda x: (x[0][1], x[0][2])):
             if dst == me:
                 continue
-            reqs.append(dist.isend(torch.from_numpy(np.ascontiguousarray(data)), dst=dst,
-                                   group=group, tag=owner * 4096 + pos))
+            for q, part in enumerate(data if isinstance(data, tuple) else (data,)):
+                if part.size:
+                    reqs.append(dist.isend(torch.from_numpy(np.ascontiguousarray(part)), dst=dst,
+                                           group=group, tag=(owner * 4096 + pos) * 2 + q))
         for r in reqs:
             r.wait()
         return {key: v.numpy() for key, v in recv.items()}
 
 
-def _pack(header: dict, payload: np.ndarray, state: bytes = b"") -> np.ndarray:
-    """Slice file: magic, u64 header length, JSON header (whose
-    ``state_bytes`` gives the length of what follows), the serialized hollow
-    state (empty for a plain tensor list), then the slice bytes."""
+def _pack_head(header: dict, state: bytes = b"") -> np.ndarray:
+    """The bytes of a slice file before its payload: magic, u64 header
+    length, JSON header (whose ``state_bytes`` gives the length of what
+    follows), then the serialized hollow state (empty for a plain tensor
+    list).  The slice bytes follow it in the file."""
     h = json.dumps({**header, "state_bytes": len(state)}, sort_keys=True).encode()
-    start = len(_MAGIC) + 8
-    out = np.empty(start + len(h) + len(state) + payload.size, np.uint8)
-    out[: len(_MAGIC)] = np.frombuffer(_MAGIC, np.uint8)
-    out[len(_MAGIC): start] = np.frombuffer(np.uint64(len(h)).tobytes(), np.uint8)
-    out[start: start + len(h)] = np.frombuffer(h, np.uint8)
-    if state:
-        out[start + len(h): start + len(h) + len(state)] = np.frombuffer(state, np.uint8)
-    out[start + len(h) + len(state):] = payload
-    return out
+    return np.frombuffer(_MAGIC + np.uint64(len(h)).tobytes() + h + state, np.uint8)
+
+
+def _pack(header: dict, payload: np.ndarray, state: bytes = b"") -> np.ndarray:
+    """A whole slice file in one array (head, then the slice bytes)."""
+    return np.concatenate([_pack_head(header, state), payload.reshape(-1)])
 
 
 def _unpack(blob: np.ndarray) -> Tuple[dict, bytes, np.ndarray]:
@@ -692,26 +701,32 @@ class ECLocalCheckpointManager:
         return None
 
     def _blobs(self, meta: dict, slices, hollow: bytes, common: dict,
-               iteration: int) -> Dict[int, np.ndarray]:
+               iteration: int) -> Dict[int, Tuple[np.ndarray, np.ndarray]]:
+        """Each slice as (file head, payload): the payload stays the codec's
+        array, which is sent and written as it is."""
         meta = {**meta, "common": common, "owner": self.rank, "iteration": iteration}
-        return {p: _pack({**meta, "pos": p}, sl, hollow) for p, sl in enumerate(slices)}
+        return {p: (_pack_head({**meta, "pos": p}, hollow), sl.reshape(-1))
+                for p, sl in enumerate(slices)}
 
-    def _place(self, blobs: Optional[Dict[int, np.ndarray]],
-               group) -> Optional[Dict[Tuple[int, int], np.ndarray]]:
-        """Every rank's blob sizes to every rank (-1: that rank failed), then,
-        if none failed, the exchange: {(owner, pos): blob} this rank holds.
+    def _place(self, blobs: Optional[Dict[int, Tuple[np.ndarray, np.ndarray]]],
+               group) -> Optional[Dict[Tuple[int, int], object]]:
+        """Every rank's (head, payload) sizes to every rank (-1: that rank
+        failed), then, if none failed, the exchange: {(owner, pos): blob} this
+        rank holds (a received array, or this rank's own (head, payload)).
         None on every rank if any rank failed.  Collective over ``group``."""
         st, me = self.strategy, self.rank
         n = st.k + st.m
-        sizes = torch.full((n,), -1, dtype=torch.int64) if blobs is None else \
-            torch.tensor([blobs[p].size for p in range(n)], dtype=torch.int64)
+        sizes = torch.full((n, 2), -1, dtype=torch.int64) if blobs is None else \
+            torch.tensor([[blobs[p][0].size, blobs[p][1].size] for p in range(n)],
+                         dtype=torch.int64)
         ranks = st.ranks()
         all_sizes = [torch.empty_like(sizes) for _ in ranks]
         dist.all_gather(all_sizes, sizes, group=group)
-        if any(int(sz[0]) < 0 for sz in all_sizes):
+        if any(int(sz[0, 0]) < 0 for sz in all_sizes):
             return None
         outgoing = {(st.holder(me, p), me, p): blobs[p] for p in range(n)}
-        incoming = [(owner, owner, p, int(sz[p])) for owner, sz in zip(ranks, all_sizes)
+        incoming = [(owner, owner, p, (int(sz[p, 0]), int(sz[p, 1])))
+                    for owner, sz in zip(ranks, all_sizes)
                     for p in range(n) if st.holder(owner, p) == me]
         received = {(owner, p): buf for (_, owner, p), buf in
                     st._exchange(outgoing, incoming, group).items()}
@@ -721,9 +736,12 @@ class ECLocalCheckpointManager:
         return received
 
     def _jobs(self, iteration: int, received):
-        jobs = [(str(self._slice_path(iteration, owner, p)), torch.from_numpy(blob))
+        """(path, [CPU uint8 tensors written one after the other]) per slice
+        file this rank holds, and the file sizes to expect."""
+        jobs = [(str(self._slice_path(iteration, owner, p)),
+                 [torch.from_numpy(part) for part in (blob if isinstance(blob, tuple) else (blob,))])
                 for (owner, p), blob in sorted(received.items())]
-        return jobs, [(path, int(t.numel())) for path, t in jobs]
+        return jobs, [(path, sum(int(t.numel()) for t in parts)) for path, parts in jobs]
 
     def _background_group(self):
         """A gloo group over the strategy's ranks for the background thread's
@@ -904,14 +922,16 @@ def _await_marker(path: str, timeout: float = 3600.0) -> None:
         time.sleep(0.01)
 
 
-def _write_slice_files(jobs: Sequence[Tuple[str, torch.Tensor]]) -> None:
-    """``async_fn`` of an asynchronous save: write each (path, uint8 CPU
-    tensor) pair atomically (tmp + rename).  No GPU work; module-level with
-    picklable arguments, so it can run in a forked or a spawned writer."""
-    for path, data in jobs:
+def _write_slice_files(jobs: Sequence[Tuple[str, Sequence[torch.Tensor]]]) -> None:
+    """``async_fn`` of an asynchronous save: write each file from its uint8
+    CPU tensors, one after the other, atomically (tmp + rename).  No GPU
+    work; module-level with picklable arguments, so it can run in a forked or
+    a spawned writer."""
+    for path, parts in jobs:
         tmp = path + ".tmp"
         with open(tmp, "wb") as f:
-            f.write(memoryview(data.numpy()))
+            for t in parts:
+                f.write(memoryview(t.numpy()))
         os.replace(tmp, path)
 
 

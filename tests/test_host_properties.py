@@ -56,6 +56,22 @@ def test_slice_format_round_trip(header, state, payload):
     h, s, p = ck._unpack(blob)
     assert s == state and bytes(p) == payload
     assert h == {**header, "state_bytes": len(state)}
+    # a save sends and writes the head and the payload as separate parts
+    assert bytes(ck._pack_head(header, state)) + payload == bytes(blob)
+
+
+def test_slice_files_written_from_parts(tmp_path):
+    """_write_slice_files writes a file's parts back to back, atomically
+    (no temporary file is left)."""
+    import torch
+    head = ck._pack_head({"pos": 3, "owner": 1}, b"hollow")
+    payload = np.arange(1000, dtype=np.uint8)
+    path = str(tmp_path / "iter_0000001_1_local.ec3")
+    ck._write_slice_files([(path, [torch.from_numpy(head), torch.from_numpy(payload)])])
+    blob = np.fromfile(path, np.uint8)
+    h, st, p = ck._unpack(blob)
+    assert h["pos"] == 3 and st == b"hollow" and np.array_equal(p, payload)
+    assert sorted(f.name for f in tmp_path.iterdir()) == ["iter_0000001_1_local.ec3"]
 
 
 def test_slice_format_rejects_foreign_bytes():
