@@ -548,7 +548,7 @@ def _pack_head(header: dict, state: bytes = b"") -> np.ndarray:
     follows), then the serialized hollow state (empty for a plain tensor
     list).  The slice bytes follow it in the file."""
     h = json.dumps({**header, "state_bytes": len(state)}, sort_keys=True).encode()
-    return np.frombuffer(_MAGIC + np.uint64(len(h)).tobytes() + h + state, np.uint8)
+    return np.frombuffer(_MAGIC + np.uint64(len(h)).tobytes() + h + state, np.uint8).copy()
 
 
 def _pack(header: dict, payload: np.ndarray, state: bytes = b"") -> np.ndarray:
