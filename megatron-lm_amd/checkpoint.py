@@ -117,11 +117,18 @@ class PendingSlices:
     staging and returns ``(meta, slices)`` (or raises what the staging
     raised)."""
 
-    def __init__(self, meta: dict, coded: torch.cuda.Event, stage: Callable[[], list]):
+    def __init__(self, meta: dict, coded: torch.cuda.Event,
+                 stage: Optional[Callable[[], list]] = None, slices: Optional[list] = None):
+        """``stage`` runs in the background thread; without it the slices
+        are given and the result is ready at once."""
         self.meta, self.coded = meta, coded
-        self._slices: Optional[list] = None
+        self._slices: Optional[list] = slices
         self._error: Optional[BaseException] = None
         self._done = threading.Event()
+        self._thread: Optional[threading.Thread] = None
+        if stage is None:
+            self._done.set()
+            return
         self._thread = threading.Thread(target=self._run, args=(stage,), daemon=True,
                                         name="ec-stage")
         self._thread.start()
@@ -140,7 +147,8 @@ class PendingSlices:
     def result(self, timeout: Optional[float] = None) -> Tuple[dict, List[np.ndarray]]:
         if not self._done.wait(timeout):
             raise TimeoutError("checkpoint slices still being staged")
-        self._thread.join()
+        if self._thread is not None:
+            self._thread.join()
         if self._error is not None:
             raise self._error
         return self.meta, self._slices
@@ -180,11 +188,13 @@ class GpuSliceCodec:
     in a background thread while training goes on.  Transfers use that side
     stream too, so they never queue behind (or in front of) training work."""
 
-    def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30):
+    def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30,
+                 snapshot_bytes: Optional[int] = None):
         from . import layout as _layout
         self._layout = _layout
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.chunk_bytes = chunk_bytes
+        self.snapshot_bytes = snapshot_bytes
         self._host: Optional[np.ndarray] = None
         self._host_lock = threading.Lock()
 
@@ -324,22 +334,39 @@ class GpuSliceCodec:
         data) runs on the device's side stream (its own hardware queue) after
         the work already enqueued on torch's current stream; with ``hold`` the
         current stream then waits for it, so later work there (the next
-        optimizer step) cannot change the tensors before they are coded.  That wait is the whole stall of a
-        save: the block is (k + m) / k of the state in HBM, written at HBM
-        speed.  A background thread moves the block to host memory as
-        ``encode`` does and frees it; ``PendingSlices.result()`` returns
-        ``(meta, slices)`` as ``encode`` would.  Without ``hold`` the caller
-        must order its own writes after ``PendingSlices.coded``."""
+        optimizer step) cannot change the tensors before they are coded.  That
+        wait is the whole stall of a save: the block is (k + m) / k of the
+        state in HBM, written at HBM speed.  A background thread moves the
+        block to host memory as ``encode`` does and frees it;
+        ``PendingSlices.result()`` returns ``(meta, slices)`` as ``encode``
+        would.  Without ``hold`` the caller must order its own writes after
+        ``PendingSlices.coded``.
+
+        When the block is larger than ``snapshot_bytes`` or the allocator
+        cannot provide it, the state is coded and staged by ``encode`` before
+        this returns (the bounded chunked path: a longer stall, the same
+        slices), and the result is ready at once."""
         from . import _lib
         from .codec import side_stream, stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
         lay = self._layout.StripeLayout(tensors, k, m, U)
         S, dev = lay.n_stripes, lay.device
-        side = side_stream(dev)
         cur = torch.cuda.current_stream(dev)
+        block = None
+        if self.snapshot_bytes is None or (k + m) * S * U <= self.snapshot_bytes:
+            try:
+                with torch.cuda.device(dev):
+                    block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
+            except torch.OutOfMemoryError:
+                block = None
+        if block is None:
+            meta, slices = self.encode(tensors)
+            coded = torch.cuda.Event()
+            coded.record(cur)
+            return PendingSlices(meta, coded, slices=slices)
+        side = side_stream(dev)
         with torch.cuda.device(dev):
-            block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
             pp = self._dev(np.stack([self._rows(block, k + i) for i in range(m)], axis=1),
                            np.int64, dev)
             gp = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1),

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import warnings
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -61,7 +62,8 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
     hardware queues with the current stream, and work on one queue runs in
     order.  ``cus`` > 0 restricts it to the first ``cus`` CUs.  One stream per
     (device, cus), created on first use and kept for the life of the process
-    (the runtime hands out few such queues)."""
+    (the runtime hands out few such queues).  If the runtime refuses one, a
+    warning says so and a stream from torch's pool stands in."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None \
         else torch.device(device)
     if dev.type != "cuda":
@@ -72,9 +74,15 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
         s = _side.get(key)
         if s is None:
             h = ctypes.c_void_p()
-            _lib.check(_lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h)),
-                       "ec_stream_create")
-            s = _side[key] = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
+            status = _lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h))
+            if status == _lib.EC_OK:
+                s = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
+            else:  # the kernels still run; only the overlap with training is lost
+                warnings.warn(f"ec_stream_create on device {idx}: {_lib.strerror(status)}; "
+                              "checkpoint work uses a stream from torch's pool, which may run "
+                              "behind the training stream's work", RuntimeWarning)
+                s = torch.cuda.Stream(device=torch.device("cuda", idx))
+            _side[key] = s
         return s
 
 

@@ -153,3 +153,19 @@ def test_gpu_side_stream(pkg, dev):
         out = pkg.rs_encode(data, 3, stream=s)
         s.synchronize()
         assert all(torch.equal(x, y) for x, y in zip(out, ref))
+
+
+def test_gpu_snapshot_falls_back_to_chunks(pkg, dev):
+    """A block over snapshot_bytes is coded by the chunked encode before
+    snapshot() returns: the same slices, ready at once."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    cpu = make_tensors(2)
+    gpu = [t.to(dev) for t in cpu]
+    codec = GpuSliceCodec(4, 2, 1024, chunk_bytes=2 * 6 * 1024, snapshot_bytes=0)
+    pending = codec.snapshot(gpu)
+    assert pending.done()
+    for t in gpu:
+        bump(t)
+    meta, slices = pending.result(timeout=60)
+    ometa, oslices = OracleSliceCodec(4, 2, 1024).encode(cpu)
+    assert meta == ometa and all(np.array_equal(a, b) for a, b in zip(slices, oslices))
