@@ -46,8 +46,9 @@ int main(int argc, char** argv) {
   enum { K = 6, M = 3 };
   const uint64_t n = argc > 1 ? strtoull(argv[1], NULL, 0) : (1u << 20) + 3;
   if (ec_abi_version() != EC_ABI_VERSION) return 4;
-  hipStream_t st;
-  CHECK_HIP(hipStreamCreate(&st));
+  /* a stream with its own hardware queue, as checkpoint work beside training uses */
+  ec_stream_t st;
+  CHECK_EC(ec_stream_create(0, 0, &st));
 
   uint8_t* host[K + M];
   uint8_t* dev[K + M];
@@ -63,8 +64,8 @@ int main(int argc, char** argv) {
   /* encode */
   uint8_t coeff[M * K];
   CHECK_EC(ec_cauchy_matrix(K, M, coeff));
-  CHECK_EC(ec_rs_encode(coeff, K, M, (const uint8_t* const*)dev, dev + K, n, (ec_stream_t)st));
-  CHECK_HIP(hipStreamSynchronize(st));
+  CHECK_EC(ec_rs_encode(coeff, K, M, (const uint8_t* const*)dev, dev + K, n, st));
+  CHECK_HIP(hipStreamSynchronize((hipStream_t)st));
   for (int i = 0; i < M; ++i) CHECK_HIP(hipMemcpy(host[K + i], dev[K + i], n, hipMemcpyDeviceToHost));
 
   /* lose shards 1, 4 and 7 (two data, one parity), rebuild them */
@@ -76,8 +77,8 @@ int main(int argc, char** argv) {
   for (int s = 0; s < K; ++s) sv[s] = dev[surv[s]];
   uint8_t* out[3];
   for (int r = 0; r < 3; ++r) CHECK_HIP(hipMalloc((void**)&out[r], n));
-  CHECK_EC(ec_rs_decode(rows, K, 3, sv, out, n, (ec_stream_t)st));
-  CHECK_HIP(hipStreamSynchronize(st));
+  CHECK_EC(ec_rs_decode(rows, K, 3, sv, out, n, st));
+  CHECK_HIP(hipStreamSynchronize((hipStream_t)st));
   uint8_t* chk = (uint8_t*)malloc(n);
   for (int r = 0; r < 3; ++r) {
     CHECK_HIP(hipMemcpy(chk, out[r], n, hipMemcpyDeviceToHost));
@@ -88,8 +89,8 @@ int main(int argc, char** argv) {
   }
 
   /* XOR parity of the first 4 shards, checked against a host XOR */
-  CHECK_EC(ec_xor_encode((const uint8_t* const*)dev, 4, out[0], n, (ec_stream_t)st));
-  CHECK_HIP(hipStreamSynchronize(st));
+  CHECK_EC(ec_xor_encode((const uint8_t* const*)dev, 4, out[0], n, st));
+  CHECK_HIP(hipStreamSynchronize((hipStream_t)st));
   CHECK_HIP(hipMemcpy(chk, out[0], n, hipMemcpyDeviceToHost));
   for (uint64_t b = 0; b < n; ++b) {
     if (chk[b] != (uint8_t)(host[0][b] ^ host[1][b] ^ host[2][b] ^ host[3][b])) {
@@ -107,7 +108,7 @@ int main(int argc, char** argv) {
   }
   for (int r = 0; r < 3; ++r) CHECK_HIP(hipFree(out[r]));
   free(chk);
-  CHECK_HIP(hipStreamDestroy(st));
+  CHECK_EC(ec_stream_destroy(st));
   printf("ec_abi_demo ok (%llu-byte shards)\n", (unsigned long long)n);
   return 0;
 }
