@@ -11,6 +11,7 @@ used by ``manager.save`` at megatron/training/checkpointing.py:538-541 and
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import threading
 import warnings
@@ -55,6 +56,17 @@ _side: Dict[Tuple[int, int], torch.cuda.ExternalStream] = {}
 _side_lock = threading.Lock()
 
 
+def _release_side_streams() -> None:
+    """At interpreter exit: finish and destroy the streams of
+    ``side_stream`` while the HIP runtime is still whole."""
+    with _side_lock:
+        for s in _side.values():
+            if isinstance(s, torch.cuda.ExternalStream):
+                s.synchronize()
+                _lib.lib().ec_stream_destroy(ctypes.c_void_p(s.cuda_stream))
+        _side.clear()
+
+
 def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
     """A stream of ``device`` with a hardware queue of its own
     (``ec_stream_create``), for checkpoint work that should run beside the
@@ -76,6 +88,8 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
             h = ctypes.c_void_p()
             status = _lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h))
             if status == _lib.EC_OK:
+                if not _side:
+                    atexit.register(_release_side_streams)
                 s = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
             else:  # the kernels still run; only the overlap with training is lost
                 warnings.warn(f"ec_stream_create on device {idx}: {_lib.strerror(status)}; "
