@@ -46,6 +46,7 @@ the ``codec`` argument exists so the exchange can be tested without a GPU.
 """
 from __future__ import annotations
 
+import atexit
 import io
 import json
 import os
@@ -53,6 +54,7 @@ import re
 import sys
 import threading
 import time
+import weakref
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
@@ -110,6 +112,17 @@ def _dtype(name: str) -> torch.dtype:
 
 # ----------------------------------------------------------------- codec --
 
+_staging_threads: "weakref.WeakSet[threading.Thread]" = weakref.WeakSet()
+_staging_join_registered = False
+
+
+def _join_staging_threads() -> None:
+    """At interpreter exit: let background staging finish before the side
+    streams it uses are destroyed (registered after them, so it runs first)."""
+    for t in list(_staging_threads):
+        t.join()
+
+
 class PendingSlices:
     """The slices of a ``GpuSliceCodec.snapshot``, being staged to host memory
     by a background thread.  ``coded`` is the device event after which the
@@ -131,6 +144,11 @@ class PendingSlices:
             return
         self._thread = threading.Thread(target=self._run, args=(stage,), daemon=True,
                                         name="ec-stage")
+        global _staging_join_registered
+        if not _staging_join_registered:
+            atexit.register(_join_staging_threads)
+            _staging_join_registered = True
+        _staging_threads.add(self._thread)
         self._thread.start()
 
     def _run(self, stage) -> None:
