@@ -463,6 +463,45 @@ def pmc_launches(pkg, dev) -> int:
     return 0
 
 
+def gf_variants(pkg, synth, dev, seed: int, steps: int) -> int:
+    """The product's GF(2^8) multiply (v_perm tables, rs_kernel) against the
+    textbook LDS log/exp tables (libec_probe.so's logexp_kernel, same grid,
+    tile order and memory instructions) on config 2's shards: HIP events per
+    launch and a byte comparison of the parity."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(pkg.library_path()), "libec_probe.so"))
+    lib.ecp_rs_logexp.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    k, m, shard = 6, 3, 256 * MiB
+    data = [torch.from_numpy(h).to(dev) for h in synth.rs_shards(seed, shard, k)]
+    coeff = pkg.cauchy_matrix(k, m)
+    ref = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
+    alt = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
+    src = (ctypes.c_void_p * k)(*[t.data_ptr() for t in data])
+    dst = (ctypes.c_void_p * m)(*[t.data_ptr() for t in alt])
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def logexp():
+        rc = lib.ecp_rs_logexp(coeff.ctypes.data_as(ctypes.c_void_p), k, m, src, dst, shard, st)
+        if rc != 0:
+            raise RuntimeError(f"ecp_rs_logexp returned {rc}")
+
+    _, vperm_ms = timed(lambda: pkg.matvec(coeff, data, out=ref), steps, 5)
+    _, lds_ms = timed(logexp, steps, 5)
+    torch.cuda.synchronize()
+    if not all(torch.equal(a, b) for a, b in zip(ref, alt)):
+        raise AssertionError("LDS log/exp parity differs from the product's")
+    traffic = (k + m) * shard
+    print(json.dumps({"mode": "gf-variants",
+                      "vperm_rs_kernel_us": round(vperm_ms * 1e3, 2),
+                      "vperm_traffic_GBps": round(traffic / (vperm_ms * 1e-3) / 1e9, 1),
+                      "lds_logexp_kernel_us": round(lds_ms * 1e3, 2),
+                      "lds_logexp_traffic_GBps": round(traffic / (lds_ms * 1e-3) / 1e9, 1),
+                      "parity_equal": True}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -473,13 +512,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
-    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched", "batched-pmc"],
+    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched", "batched-pmc",
+                                       "gf-variants"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
                          "plain 256 MiB copy and of the RS(6,3) encode, for counter runs; "
                          "batched: configs 4 and 5 only; batched-pmc: the copy plus 3 "
-                         "launches of the config-5 encode, for counter runs")
+                         "launches of the config-5 encode, for counter runs; gf-variants: "
+                         "the v_perm GF multiply against LDS log/exp tables")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the erasure-coding path has no multi-GPU "
@@ -504,6 +545,8 @@ def main() -> int:
         return 0
     if args.mode == "batched-pmc":
         return batched_pmc_launches(pkg, synth, dev, args.seed)
+    if args.mode == "gf-variants":
+        return gf_variants(pkg, synth, dev, args.seed, min(args.steps, 50))
 
     # ---- config 2: RS(6,3), 6 x 256 MiB fp32 optimizer state -------------
     k, m, shard = 6, 3, 256 * MiB
