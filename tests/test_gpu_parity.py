@@ -513,3 +513,37 @@ def test_encode_batched_copy(pkg, dev, k, m, unit, misalign):
                 piece = host[t][i * unit: (i + 1) * unit]
                 want[: piece.size] = piece
             assert np.array_equal(got[j, s], want), (s, j)
+
+
+@pytest.mark.parametrize("unit", [4096, 16384])
+def test_encode_batched_copy_every_instantiated_shape(pkg, dev, unit):
+    """Every fixed-size (k, m) of the copying encode, with 4 KiB tiles and,
+    for k <= 8 and 16 KiB units, 16 KiB tiles: parity against the oracle and
+    the data rows against the zero-padded units."""
+    from megatron_lm_amd import _lib
+    rng = np.random.default_rng(unit)
+    for k in range(1, 17):
+        host, tensors = _ragged_device(rng, dev, k + 3, 3 * unit)
+        for m in range(1, 5):
+            lay = pkg.StripeLayout(tensors, k, m, unit)
+            S = lay.n_stripes
+            block = torch.empty((k + m, S, unit), dtype=torch.uint8, device=dev)
+            base = np.uint64(block.data_ptr())
+            rows = np.arange(S, dtype=np.uint64)[:, None] * np.uint64(unit)
+            pp = base + (np.arange(k, k + m, dtype=np.uint64)[None, :] * np.uint64(S * unit)) + rows
+            cp = base + (np.arange(k, dtype=np.uint64)[None, :] * np.uint64(S * unit)) + rows
+            d_pp = torch.from_numpy(np.ascontiguousarray(pp).view(np.int64)).to(dev)
+            d_cp = torch.from_numpy(np.ascontiguousarray(cp).view(np.int64)).to(dev)
+            _lib.check(_lib.lib().ec_encode_batched_copy(
+                _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+                d_pp.data_ptr(), d_cp.data_ptr(), S, unit, None), "ec_encode_batched_copy")
+            torch.cuda.synchronize()
+            got = block.cpu().numpy()
+            assert np.array_equal(got[k:].transpose(1, 0, 2),
+                                  _oracle_layout_parity(lay, host, unit)), (k, m)
+            stream = np.zeros(S * k * unit, np.uint8)
+            for u in range(lay.n_units):
+                t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+                piece = host[t][i * unit: (i + 1) * unit]
+                stream[u * unit: u * unit + piece.size] = piece
+            assert np.array_equal(got[:k].transpose(1, 0, 2).reshape(-1), stream), (k, m)
