@@ -126,16 +126,16 @@ def _join_staging_threads() -> None:
 class PendingSlices:
     """The slices of a ``GpuSliceCodec.snapshot``, being staged to host memory
     by a background thread.  ``coded`` is the device event after which the
-    tensors may change; ``meta`` is known at once; ``result()`` waits for the
-    staging and returns ``(meta, slices)`` (or raises what the staging
-    raised)."""
+    tensors may change; ``result()`` waits for the staging and returns
+    ``(meta, slices)`` (or raises what the staging raised)."""
 
-    def __init__(self, meta: dict, coded: torch.cuda.Event,
-                 stage: Optional[Callable[[], list]] = None, slices: Optional[list] = None):
-        """``stage`` runs in the background thread; without it the slices
-        are given and the result is ready at once."""
-        self.meta, self.coded = meta, coded
-        self._slices: Optional[list] = slices
+    def __init__(self, coded: torch.cuda.Event,
+                 stage: Optional[Callable[[], Tuple[dict, list]]] = None,
+                 ready: Optional[Tuple[dict, list]] = None):
+        """``stage`` runs in the background thread and returns ``(meta,
+        slices)``; without it ``ready`` is the result, available at once."""
+        self.coded = coded
+        self._result: Optional[Tuple[dict, list]] = ready
         self._error: Optional[BaseException] = None
         self._done = threading.Event()
         self._thread: Optional[threading.Thread] = None
@@ -153,7 +153,7 @@ class PendingSlices:
 
     def _run(self, stage) -> None:
         try:
-            self._slices = stage()
+            self._result = stage()
         except BaseException as e:  # noqa: BLE001 - handed to result()
             self._error = e
         finally:
@@ -169,7 +169,7 @@ class PendingSlices:
             self._thread.join()
         if self._error is not None:
             raise self._error
-        return self.meta, self._slices
+        return self._result
 
 
 class GpuSliceCodec:
@@ -379,10 +379,10 @@ class GpuSliceCodec:
             except torch.OutOfMemoryError:
                 block = None
         if block is None:
-            meta, slices = self.encode(tensors)
+            ready = self.encode(tensors)
             coded = torch.cuda.Event()
             coded.record(cur)
-            return PendingSlices(meta, coded, slices=slices)
+            return PendingSlices(coded, ready=ready)
         side = side_stream(dev)
         with torch.cuda.device(dev):
             pp = self._dev(np.stack([self._rows(block, k + i) for i in range(m)], axis=1),
@@ -405,14 +405,17 @@ class GpuSliceCodec:
 
         def stage():
             nonlocal block
+            # tensor shapes and dtypes cannot change in place: read them here,
+            # off the caller's critical path
+            meta = self._meta(lay, tensors)
             out = self._host_out((k + m, S * U))
             with torch.cuda.device(dev), self._pool() as pool:
                 self._to_host(k + m, chunks, C, lambda n: block[:, chunks[n][0]:sum(chunks[n])],
                               out, side, pool)
             block = None   # back to the allocator: the last transfer has landed
-            return [out[p] for p in range(k + m)]
+            return meta, [out[p] for p in range(k + m)]
 
-        return PendingSlices(self._meta(lay, tensors), coded, stage)
+        return PendingSlices(coded, stage)
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib

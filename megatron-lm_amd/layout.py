@@ -51,6 +51,24 @@ def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
     return unit_tensor, unit_index, ptr.reshape(n_stripes, k), ln.reshape(n_stripes, k)
 
 
+def _spans(tensors: Sequence[torch.Tensor], device) -> Tuple[np.ndarray, np.ndarray]:
+    """(base addresses, byte sizes) of contiguous HIP tensors on ``device``,
+    with as few calls into torch per tensor as the checks allow (a save codes
+    thousands of tensors); a tensor that fails a check gets codec._dev's
+    error."""
+    idx = torch.device(device).index if device is not None else None
+    tensor = torch.Tensor
+    ptrs, sizes = [], []
+    for i, t in enumerate(tensors):
+        if not isinstance(t, tensor) or t.get_device() != idx or idx is None or \
+                not t.is_contiguous():
+            _dev(t, f"tensors[{i}]", device)
+            raise ValueError(f"tensors[{i}] is not a contiguous tensor on {device}")
+        ptrs.append(t.data_ptr())
+        sizes.append(t.nbytes)
+    return np.array(ptrs, np.uint64).reshape(-1), np.array(sizes, np.int64).reshape(-1)
+
+
 @dataclass
 class BatchPlan:
     """Device descriptors of one batched decode or update launch."""
@@ -90,11 +108,7 @@ class StripeLayout:
         else:  # an empty list codes as one stripe of absent (zero) units
             self.device = torch.device(device) if device is not None else \
                 torch.device("cuda", torch.cuda.current_device())
-        base = np.zeros(len(self.tensors), np.uint64)
-        size = np.zeros(len(self.tensors), np.int64)
-        for i, t in enumerate(self.tensors):
-            p, nb = _dev(t, f"tensors[{i}]", self.device)
-            base[i], size[i] = p, nb
+        base, size = _spans(self.tensors, self.device)
         self.tensor_bytes = size
         (self.unit_tensor, self.unit_index, self.host_ptrs,
          self.host_len) = unit_table(base, size, k, unit_bytes)

@@ -20,7 +20,7 @@ class _Staged:
     when its result is asked for, as a staging error would)."""
 
     def __init__(self, meta, slices, error=None):
-        self.meta, self._slices, self._error = meta, slices, error
+        self._meta, self._slices, self._error = meta, slices, error
 
     def done(self):
         return True
@@ -28,7 +28,7 @@ class _Staged:
     def result(self, timeout=None):
         if self._error is not None:
             raise self._error
-        return self.meta, self._slices
+        return self._meta, self._slices
 
 
 class OracleSliceCodec:
