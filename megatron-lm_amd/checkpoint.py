@@ -239,6 +239,17 @@ class GpuSliceCodec:
         return np.uint64(block[p].data_ptr()) + np.arange(S, dtype=np.uint64) * np.uint64(U)
 
     @staticmethod
+    def _row_ptrs(block: torch.Tensor, first: int, count: int) -> torch.Tensor:
+        """[stripes, count] device addresses of the units of rows first ..
+        first + count - 1 of a (rows, stripes, unit_bytes) device block,
+        computed on the device (no host array, no upload)."""
+        _, S, U = block.shape
+        stripe = torch.arange(S, dtype=torch.int64, device=block.device).unsqueeze(1) * U
+        row = torch.arange(first, first + count, dtype=torch.int64,
+                           device=block.device).unsqueeze(0) * (S * U)
+        return (stripe + row).add_(block.data_ptr())
+
+    @staticmethod
     def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
 
@@ -385,10 +396,8 @@ class GpuSliceCodec:
             return PendingSlices(coded, ready=ready)
         side = side_stream(dev)
         with torch.cuda.device(dev):
-            pp = self._dev(np.stack([self._rows(block, k + i) for i in range(m)], axis=1),
-                           np.int64, dev)
-            gp = self._dev(np.stack([self._rows(block, p) for p in range(k)], axis=1),
-                           np.int64, dev)
+            pp = self._row_ptrs(block, k, m)
+            gp = self._row_ptrs(block, 0, k)
         for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
             t.record_stream(side)
         side.wait_stream(cur)   # the tensors' producers and the descriptor uploads

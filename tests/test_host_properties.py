@@ -109,3 +109,14 @@ def test_placement(g, k, m, jump):
     if g % jump == 0 and g // jump >= k + m:
         for owner in range(g):
             assert len({s.holder(owner, p) // jump for p in range(k + m)}) == k + m
+
+
+def test_row_addresses_on_device_match_host():
+    """The snapshot's device-computed unit addresses equal the host ones."""
+    import torch
+    block = torch.empty((7, 5, 48), dtype=torch.uint8)
+    for first, count in ((0, 4), (4, 3), (2, 1)):
+        want = np.stack([ck.GpuSliceCodec._rows(block, p) for p in range(first, first + count)],
+                        axis=1).view(np.int64)
+        got = ck.GpuSliceCodec._row_ptrs(block, first, count).numpy()
+        assert np.array_equal(got, want), (first, count)
