@@ -51,6 +51,15 @@ def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
     return unit_tensor, unit_index, ptr.reshape(n_stripes, k), ln.reshape(n_stripes, k)
 
 
+def _upload(a: np.ndarray, device) -> torch.Tensor:
+    """A device copy of a host array, enqueued on the current stream from
+    pinned memory (torch keeps the pinned block until the copy has run)."""
+    src = torch.from_numpy(np.ascontiguousarray(a))
+    pinned = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+    pinned.copy_(src)
+    return pinned.to(device, non_blocking=True)
+
+
 def _spans(tensors: Sequence[torch.Tensor], device) -> Tuple[np.ndarray, np.ndarray]:
     """(base addresses, byte sizes) of contiguous HIP tensors on ``device``,
     with as few calls into torch per tensor as the checks allow (a save codes
@@ -115,8 +124,14 @@ class StripeLayout:
         self.n_units = int(self.unit_tensor.size)
         self.n_stripes = self.host_ptrs.shape[0]
         self.data_bytes = int(size.sum())
-        self.d_ptrs = torch.from_numpy(self.host_ptrs.view(np.int64).copy()).to(self.device)
-        self.d_len = torch.from_numpy(self.host_len.view(np.int32).copy()).to(self.device)
+        # Through pinned memory, asynchronously on the device's current stream:
+        # the host does not wait for that stream's earlier work.  Launches on
+        # another stream wait for ``uploaded`` first.
+        with torch.cuda.device(self.device):
+            self.d_ptrs = _upload(self.host_ptrs.view(np.int64), self.device)
+            self.d_len = _upload(self.host_len.view(np.int32), self.device)
+            self.uploaded = torch.cuda.Event()
+            self.uploaded.record()
 
     # ------------------------------------------------------------ parity --
 
@@ -140,6 +155,8 @@ class StripeLayout:
         else:
             self._parity_ptrs_check(parity)
         pp = cached[1]
+        if stream is not None:
+            stream.wait_event(self.uploaded)
         _lib.check(_lib.lib().ec_encode_batched(
             _lib.u8ptr(self.coeff), self.k, self.m, self.d_ptrs.data_ptr(), self.d_len.data_ptr(),
             pp.data_ptr(), self.n_stripes, self.unit_bytes, stream_handle(stream, self.device)),
