@@ -463,6 +463,76 @@ def pmc_launches(pkg, dev) -> int:
     return 0
 
 
+def training_with_checkpoints(pkg, dev, steps: int = 40, every: int = 10) -> dict:
+    """A training loop with periodic erasure-coded checkpoints: 8 bf16-autocast
+    8192 x 8192 linear layers over 8192 tokens, fp32 parameters with AdamW
+    (the checkpointed state: parameters and both moments, 6.4 GB), one step =
+    forward, backward, optimizer step.  The same ``steps`` run three times:
+    without checkpoints, with a synchronous save (GpuSliceCodec.encode, slices
+    in host memory before training resumes) every ``every`` steps, and with a
+    snapshot save (GpuSliceCodec.snapshot: training resumes once the state is
+    coded in HBM; staging runs in the background).  Reports ms per step of
+    each and the save's overhead per save."""
+    import torch
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    torch.manual_seed(0)
+    n, layers = 8192, 8
+    model = torch.nn.Sequential(*[torch.nn.Linear(n, n, bias=False) for _ in range(layers)]).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-5)
+    x = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(x).float().pow(2).mean()
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=False)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+
+    def state():
+        return [t for p in model.parameters()
+                for t in (p.data, opt.state[p]["exp_avg"], opt.state[p]["exp_avg_sq"])]
+
+    nbytes = sum(t.numel() * t.element_size() for t in state())
+    codec = GpuSliceCodec(12, 4, 4 << 20)
+    pending = []
+
+    def run(save):
+        codec.snapshot(state()).result()          # warm: host array, pinned buffers
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step()
+            if save == "sync" and (i + 1) % every == 0:
+                codec.encode(state())
+            elif save == "snapshot" and (i + 1) % every == 0:
+                pending.append(codec.snapshot(state()))
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        for p in pending:
+            p.result()
+        pending.clear()
+        return t * 1e3 / steps
+
+    base = run(None)
+    sync = run("sync")
+    snap = run("snapshot")
+    saves = steps // every
+    res = {"train_state_GB": round(nbytes / 1e9, 2), "train_steps": steps, "train_save_every": every,
+           "train_ms_per_step": round(base, 2),
+           "train_ms_per_step_sync_saves": round(sync, 2),
+           "train_ms_per_step_snapshot_saves": round(snap, 2),
+           "train_ms_per_sync_save": round((sync - base) * steps / saves, 1),
+           "train_ms_per_snapshot_save": round((snap - base) * steps / saves, 1)}
+    del model, opt, x
+    torch.cuda.empty_cache()
+    log(f"training with checkpoints: {res}")
+    return res
+
+
 def gf_variants(pkg, synth, dev, seed: int, steps: int) -> int:
     """The product's GF(2^8) multiply (v_perm tables, rs_kernel) against the
     textbook LDS log/exp tables (libec_probe.so's logexp_kernel, same grid,
@@ -513,14 +583,15 @@ def main() -> int:
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
     ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched", "batched-pmc",
-                                       "gf-variants"],
+                                       "gf-variants", "train"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
                          "plain 256 MiB copy and of the RS(6,3) encode, for counter runs; "
                          "batched: configs 4 and 5 only; batched-pmc: the copy plus 3 "
                          "launches of the config-5 encode, for counter runs; gf-variants: "
-                         "the v_perm GF multiply against LDS log/exp tables")
+                         "the v_perm GF multiply against LDS log/exp tables; train: a training "
+                         "loop with synchronous and with snapshot checkpoint saves")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the erasure-coding path has no multi-GPU "
@@ -547,6 +618,9 @@ def main() -> int:
         return batched_pmc_launches(pkg, synth, dev, args.seed)
     if args.mode == "gf-variants":
         return gf_variants(pkg, synth, dev, args.seed, min(args.steps, 50))
+    if args.mode == "train":
+        print(json.dumps({"mode": "train", **training_with_checkpoints(pkg, dev)}), flush=True)
+        return 0
 
     # ---- config 2: RS(6,3), 6 x 256 MiB fp32 optimizer state -------------
     k, m, shard = 6, 3, 256 * MiB

@@ -222,6 +222,25 @@ int ec_stream_create(int device, int n_cus, ec_stream_t* out);
 /* Waits for the stream's work and destroys it. */
 int ec_stream_destroy(ec_stream_t stream);
 
+/* Copies a rows x row_bytes region of device memory (row pitch src_pitch)
+ * to host memory that need not be pinned (row pitch dst_pitch), through the
+ * caller's pinned buffer h_pinned of pinned_bytes: the buffer's two halves
+ * alternate, the transfer of one chunk of columns runs on `stream` while
+ * `threads` host threads copy the previous chunk out of the other half.
+ * Returns when every byte is in h_dst; the transfers follow the work
+ * already enqueued on `stream`.  EC_EINVAL for null pointers, pitches below
+ * row_bytes, threads outside [1, 64], or a pinned buffer without room for
+ * one byte of every row per half; rows or row_bytes 0 is a no-op.  No
+ * counterpart in the reference: its checkpoint D2H is
+ * copy_tensors_to_cpu (tensor_aware_state_dict.py:245-274), run in the
+ * training process before the async writer starts.  This call stages a
+ * coded checkpoint in the background while training runs in the same
+ * process, and runs whole inside the library so that it holds no
+ * interpreter lock the training thread needs (ctypes releases it). */
+int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
+                     uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
+                     uint64_t pinned_bytes, int threads, ec_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

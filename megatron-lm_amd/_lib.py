@@ -40,6 +40,7 @@ EXPORTS = (
     "ec_parity_update",
     "ec_stream_create",
     "ec_stream_destroy",
+    "ec_stage_to_host",
 )
 
 
@@ -108,6 +109,8 @@ def lib() -> ctypes.CDLL:
     L.ec_stream_create.argtypes = [_i, _i, ctypes.POINTER(_vp)]
     L.ec_stream_destroy.restype = _i
     L.ec_stream_destroy.argtypes = [_vp]
+    L.ec_stage_to_host.restype = _i
+    L.ec_stage_to_host.argtypes = [_vp, _u64, _vp, _u64, _u32, _u64, _vp, _u64, _i, _vp]
     _lib = L
     return L
 

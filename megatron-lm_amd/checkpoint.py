@@ -193,9 +193,9 @@ class GpuSliceCodec:
     Encode, per chunk: one launch writes the parity units into the device
     buffer's parity rows and, in the same pass over the data, the data units
     (zero-padded) into its data rows; the buffer goes to pinned memory on a
-    copy stream, and a thread pool moves it into the result while the next
-    chunk is coded and transferred.  Decode, per chunk: the thread pool copies the k
-    slices' part into pinned memory, the copy stream sends it up, one scatter
+    copy stream, and four threads move it into the result while the next
+    chunk is coded and transferred.  Decode, per chunk: the threads copy the
+    k slices' part into pinned memory, the copy stream sends it up, one scatter
     launch puts the data rows into fresh tensors and one decode launch
     rebuilds the lost data positions; the next chunk's host copy overlaps.
 
@@ -213,6 +213,7 @@ class GpuSliceCodec:
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.chunk_bytes = chunk_bytes
         self.snapshot_bytes = snapshot_bytes
+        self.stage_threads = 8   # host threads of a snapshot's background staging
         self._host: Optional[np.ndarray] = None
         self._host_lock = threading.Lock()
 
@@ -253,13 +254,6 @@ class GpuSliceCodec:
     def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
 
-    @staticmethod
-    def _pieces(rows: int, c0: int, c: int, U: int):
-        """(row, first byte, end byte) pieces of at most 64 MiB covering
-        stripes [c0, c0 + c) of every row."""
-        return [(r, a, min(a + (64 << 20), (c0 + c) * U))
-                for r in range(rows) for a in range(c0 * U, (c0 + c) * U, 64 << 20)]
-
     def _meta(self, lay, tensors) -> dict:
         return {"k": self.k, "m": self.m, "unit_bytes": self.unit_bytes,
                 "n_stripes": lay.n_stripes, "n_units": lay.n_units,
@@ -271,10 +265,11 @@ class GpuSliceCodec:
         unit_bytes) source into the host array ``out`` (rows, S * unit_bytes)
         through two pinned (rows, C, unit_bytes) buffers: transfers on the
         ``copy`` stream, row by row (a row's part of a chunk is contiguous),
-        then 64 MiB pieces copied out by the thread pool while the next chunk
-        is in flight.  ``src(n)`` is chunk n's device view; ``produce(n,
-        landed)``, when given, enqueues what fills it and makes ``copy`` wait
-        for that (``landed[j]`` = chunk j has reached pinned memory)."""
+        then copied into ``out`` by the pool's threads while the next chunk
+        is in flight.  ``src(n)`` is chunk n's device view;
+        ``produce(n, landed)``, when given, enqueues what fills it and makes
+        ``copy`` wait for that (``landed[j]`` = chunk j has reached pinned
+        memory)."""
         U, nb = self.unit_bytes, min(2, len(chunks))
         pins = [torch.empty((rows, C, U), dtype=torch.uint8, pin_memory=True)
                 for _ in range(nb)]
@@ -283,10 +278,9 @@ class GpuSliceCodec:
 
         def drain(n):
             c0, c = chunks[n]
-            flat = pins[n % nb].numpy().reshape(rows, -1)
             landed[n].synchronize()
-            return [pool.submit(np.copyto, out[r, a:b], flat[r, a - c0 * U:b - c0 * U])
-                    for r, a, b in self._pieces(rows, c0, c, U)]
+            pinned = pins[n % nb].numpy()[:, :c].reshape(rows, -1)
+            return _copy_rows(pool, out[:, c0 * U:(c0 + c) * U], lambda r: pinned[r])
 
         for n, (c0, c) in enumerate(chunks):
             b = n % nb
@@ -308,8 +302,9 @@ class GpuSliceCodec:
             for f in fs:
                 f.result()
 
-    def _pool(self) -> ThreadPoolExecutor:
-        return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
+    @staticmethod
+    def _pool() -> ThreadPoolExecutor:
+        return ThreadPoolExecutor(max_workers=_COPY_THREADS)
 
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         """Code and stage in bounded chunks; returns when the slices are in
@@ -317,7 +312,7 @@ class GpuSliceCodec:
         the work that produced the tensors), the transfers on the device's
         side stream."""
         from . import _lib
-        from .codec import side_stream, stream_handle
+        from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
         lay = self._layout.StripeLayout(tensors, k, m, U)
@@ -327,7 +322,9 @@ class GpuSliceCodec:
         nb = min(2, len(chunks))
         out = self._host_out((k + m, S * U))
         with torch.cuda.device(dev), self._pool() as pool:
-            comp, copy = torch.cuda.current_stream(dev), side_stream(dev)
+            # transfers on an ordinary stream: they go to the DMA engines (on a
+            # CU-masked stream they ran as shader copies on the compute units)
+            comp, copy = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
             bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
             # per buffer: parity unit (s, i) -> row k + i, data unit (s, p) -> row p
             pp = [self._dev(np.stack([self._rows(b, k + i) for i in range(m)], axis=1), np.int64,
@@ -409,8 +406,6 @@ class GpuSliceCodec:
         coded.record(side)
         if hold:
             cur.wait_event(coded)
-        C = self._chunk_stripes(S, k + m)
-        chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
 
         def stage():
             nonlocal block
@@ -418,9 +413,19 @@ class GpuSliceCodec:
             # off the caller's critical path
             meta = self._meta(lay, tensors)
             out = self._host_out((k + m, S * U))
-            with torch.cuda.device(dev), self._pool() as pool:
-                self._to_host(k + m, chunks, C, lambda n: block[:, chunks[n][0]:sum(chunks[n])],
-                              out, side, pool)
+            pinned = torch.empty(min(2 * self.chunk_bytes, 2 * (k + m) * S * U),
+                                 dtype=torch.uint8, pin_memory=True)
+            # The transfers go on an ordinary stream, after the coding: there
+            # they run on the DMA engines, beside training (on the CU-masked
+            # side stream they ran as shader copies and slowed its kernels),
+            # in one foreign call that holds no interpreter lock.
+            xfer = torch.cuda.Stream(dev)
+            xfer.wait_event(coded)
+            block.record_stream(xfer)
+            _lib.check(_lib.lib().ec_stage_to_host(
+                block.data_ptr(), S * U, out.ctypes.data, S * U, k + m, S * U,
+                pinned.data_ptr(), pinned.numel(), self.stage_threads,
+                stream_handle(xfer, dev)), "ec_stage_to_host")
             block = None   # back to the allocator: the last transfer has landed
             return meta, [out[p] for p in range(k + m)]
 
@@ -428,7 +433,7 @@ class GpuSliceCodec:
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib
-        from .codec import decode_matrix, side_stream, stream_handle
+        from .codec import decode_matrix, stream_handle
         k, m, U, S = meta["k"], meta["m"], meta["unit_bytes"], meta["n_stripes"]
         if len(slices) < k:
             raise CheckpointingException(f"only {len(slices)} of the {k} slices needed")
@@ -456,7 +461,7 @@ class GpuSliceCodec:
         one = np.ones((1, 1), np.uint8)
         hp = [p for _, p in have]
         with torch.cuda.device(device), self._pool() as pool:
-            comp, copy = torch.cuda.current_stream(device), side_stream(device)
+            comp, copy = torch.cuda.current_stream(device), torch.cuda.Stream(device)
             bufs = [torch.empty((k, C, U), dtype=torch.uint8, device=device) for _ in range(nb)]
             for bf in bufs:
                 bf.record_stream(copy)
@@ -479,10 +484,8 @@ class GpuSliceCodec:
 
             def fill(n):
                 c0, c = chunks[n]
-                flat = pins[n % nb].numpy().reshape(k, -1)
-                return [pool.submit(np.copyto, flat[r, a - c0 * U:b - c0 * U],
-                                    slices[avail[r]][a:b])
-                        for r, a, b in self._pieces(k, c0, c, U)]
+                return _copy_rows(pool, pins[n % nb].numpy()[:, :c].reshape(k, -1),
+                                  lambda r: slices[avail[r]][c0 * U:(c0 + c) * U])
 
             filling = fill(0)
             for n, (c0, c) in enumerate(chunks):
@@ -956,6 +959,23 @@ class ECLocalCheckpointManager:
             state.insert_tensors(tensors)
             return state, self._ckpt_id(it)
         return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
+
+
+_COPY_THREADS = 16   # the box's CPU share per GPU
+
+
+def _copy_rows(pool: ThreadPoolExecutor, dst: np.ndarray, src_row: Callable) -> list:
+    """dst[r] <- src_row(r) for the rows of a 2-D host array, split over the
+    pool's threads (numpy drops the GIL while it copies).  For the blocking
+    paths, whose caller waits anyway; a snapshot's background staging runs in
+    ec_stage_to_host instead.  Returns the futures."""
+    groups = np.array_split(np.arange(dst.shape[0]), min(_COPY_THREADS, dst.shape[0]))
+
+    def run(rows):
+        for r in rows:
+            np.copyto(dst[r], src_row(int(r)))
+
+    return [pool.submit(run, g) for g in groups if g.size]
 
 
 def _common(state) -> dict:

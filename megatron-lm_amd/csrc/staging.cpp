@@ -1,0 +1,99 @@
+// staging.cpp — host side of moving coded checkpoint slices out of HBM
+// (ec_stage_to_host).
+//
+// A background save stages the coded block to host memory while training
+// runs in the same process.  The whole loop (a transfer per chunk and row,
+// an event wait, host copies on several threads) runs inside one foreign
+// call, which ctypes makes with the interpreter's lock released, so the
+// staging thread takes that lock from the training thread only to start
+// and to finish.  Give it an ordinary stream: on MI355X, transfers on a
+// CU-masked stream ran as shader copies on the compute units and slowed the
+// training kernels beside them, on an ordinary stream they use the DMA
+// engines.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "ec_mi355.h"
+
+namespace {
+
+// dst[r * dst_pitch + x] = src[r * src_pitch + x] for r < rows, x < width,
+// split by rows (or by column ranges when rows < threads) over `threads`
+// host threads.
+void copy_rect(uint8_t* dst, uint64_t dst_pitch, const uint8_t* src, uint64_t src_pitch,
+               uint32_t rows, uint64_t width, int threads) {
+  // Work items: (row, column begin, column end) with about equal bytes.
+  const uint64_t total = (uint64_t)rows * width;
+  const uint64_t share = (total + threads - 1) / threads;
+  auto run = [&](int t) {
+    uint64_t begin = (uint64_t)t * share, end = std::min(total, begin + share);
+    while (begin < end) {
+      const uint64_t r = begin / width, x = begin % width;
+      const uint64_t n = std::min(end - begin, width - x);
+      memcpy(dst + r * dst_pitch + x, src + r * src_pitch + x, n);
+      begin += n;
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int t = 1; t < threads; ++t) pool.emplace_back(run, t);
+  run(0);
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
+                     uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
+                     uint64_t pinned_bytes, int threads, ec_stream_t stream) {
+  if (rows == 0 || row_bytes == 0) return EC_OK;
+  if (!d_src || !h_dst || !h_pinned || threads < 1 || threads > 64) return EC_EINVAL;
+  if (src_pitch < row_bytes || dst_pitch < row_bytes) return EC_EINVAL;
+  // Two halves of the pinned buffer, each holding `width` bytes of every row.
+  const uint64_t half = pinned_bytes / 2;
+  uint64_t width = half / rows;
+  if (width >= 4096) width -= width % 4096;  // whole pages when there is room
+  if (width == 0) return EC_EINVAL;
+  width = std::min(width, row_bytes);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  int status = EC_OK;
+  for (auto& e : ev)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
+      status = EC_EHIP;
+  const uint64_t n_chunks = (row_bytes + width - 1) / width;
+  // Chunk j: columns [j * width, min(row_bytes, (j + 1) * width)) of every
+  // row, through pinned half j % 2.  The transfer of chunk j is in flight
+  // while the threads copy chunk j - 1 out of the other half.
+  for (uint64_t j = 0; status == EC_OK && j <= n_chunks; ++j) {
+    if (j < n_chunks) {
+      const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
+      uint8_t* pin = h_pinned + (j % 2) * half;
+      for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
+        if (hipMemcpyAsync(pin + (uint64_t)r * w, d_src + (uint64_t)r * src_pitch + x0, w,
+                           hipMemcpyDeviceToHost, st) != hipSuccess)
+          status = EC_EHIP;
+      if (status == EC_OK && hipEventRecord(ev[j % 2], st) != hipSuccess) status = EC_EHIP;
+    }
+    if (status == EC_OK && j >= 1) {
+      const uint64_t p = j - 1, x0 = p * width, w = std::min(width, row_bytes - x0);
+      if (hipEventSynchronize(ev[p % 2]) != hipSuccess) {
+        status = EC_EHIP;
+        break;
+      }
+      copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
+    }
+  }
+  if (status != EC_OK) (void)hipStreamSynchronize(st);  // no transfer outlives the call
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return status;
+}
+
+}  // extern "C"

@@ -122,3 +122,17 @@ def test_missing_library_fails_loudly(pkg, monkeypatch):
     monkeypatch.setattr(pkg._lib, "LIB_PATH", "/nonexistent/libec_mi355.so")
     with pytest.raises(pkg.ECLibraryMissing):
         pkg.cauchy_matrix(6, 3)
+
+
+def test_stage_to_host_rejects_bad_arguments(pkg):
+    """Host-side validation of ec_stage_to_host (no device work)."""
+    L = pkg._lib.lib()
+    p = ctypes.c_void_p(4096)
+    assert L.ec_stage_to_host(p, 64, p, 64, 0, 64, p, 256, 4, None) == pkg._lib.EC_OK
+    assert L.ec_stage_to_host(p, 64, p, 64, 2, 0, p, 256, 4, None) == pkg._lib.EC_OK
+    assert L.ec_stage_to_host(None, 64, p, 64, 2, 64, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_host(p, 64, p, 64, 2, 64, None, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_host(p, 32, p, 64, 2, 64, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_host(p, 64, p, 64, 2, 64, p, 256, 0, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_host(p, 64, p, 64, 2, 64, p, 256, 65, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_host(p, 64, p, 64, 4, 64, p, 6, 4, None) == pkg._lib.EC_EINVAL

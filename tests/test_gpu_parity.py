@@ -547,3 +547,27 @@ def test_encode_batched_copy_every_instantiated_shape(pkg, dev, unit):
                 piece = host[t][i * unit: (i + 1) * unit]
                 stream[u * unit: u * unit + piece.size] = piece
             assert np.array_equal(got[:k].transpose(1, 0, 2).reshape(-1), stream), (k, m)
+
+
+@pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [
+    (16, (1 << 20) + 48, (1 << 20) + 64, 1 << 20, 8),   # many chunks, a short last one
+    (3, 5000, 5000, 64, 1),                             # chunks narrower than a page
+    (1, 4096, 8192, 1 << 16, 64),                       # one row, more threads than bytes/64
+])
+def test_stage_to_host(pkg, dev, rows, row_bytes, pitch, pinned, threads):
+    """ec_stage_to_host copies a pitched device region into pageable host
+    memory exactly, through a pinned buffer smaller than the region, after
+    the work already on the stream."""
+    from megatron_lm_amd import _lib
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows)
+    src = torch.randint(0, 256, (rows, pitch), dtype=torch.uint8, device=dev, generator=g)
+    out = np.full((rows, pitch + 16), 0x77, np.uint8)
+    pin = torch.empty(pinned, dtype=torch.uint8, pin_memory=True)
+    src.add_(1)   # enqueued before the call: the copy must see it
+    _lib.check(_lib.lib().ec_stage_to_host(
+        src.data_ptr(), pitch, out.ctypes.data, pitch + 16, rows, row_bytes, pin.data_ptr(),
+        pinned, threads, None), "ec_stage_to_host")
+    want = src.cpu().numpy()
+    assert np.array_equal(out[:, :row_bytes], want[:, :row_bytes])
+    assert (out[:, row_bytes:] == 0x77).all()
