@@ -69,10 +69,13 @@ def _release_side_streams() -> None:
 
 def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
     """A stream of ``device`` with a hardware queue of its own
-    (``ec_stream_create``), for checkpoint work that should run beside the
+    (``ec_stream_create``), for checkpoint kernels that should run beside the
     training stream rather than behind it: torch's pooled streams share a few
     hardware queues with the current stream, and work on one queue runs in
-    order.  ``cus`` > 0 restricts it to the first ``cus`` CUs.  One stream per
+    order.  Kernels only: copies between host and device belong on an
+    ordinary stream, where they use the DMA engines (on this CU-masked
+    stream they run as shader copies and slow the kernels beside them).
+    ``cus`` > 0 restricts it to the first ``cus`` CUs.  One stream per
     (device, cus), created on first use and kept for the life of the process
     (the runtime hands out few such queues).  If the runtime refuses one, a
     warning says so and a stream from torch's pool stands in."""
