@@ -5,8 +5,8 @@ serialized fp32 optimizer state, inputs resident in HBM, and its HBM roofline
 fraction.  Also measured in the same run and reported under
 "also": RS(6,3) decode with 3 seeded erasures, XOR parity of 4 x 64 MiB bf16
 shards, the batched configurations, the encode's interference with a GEMM
-load, the checkpoint staging path, and a streaming copy as the practical
-bandwidth ceiling.  The
+load, the checkpoint staging path and snapshot saves, a training loop with
+periodic saves, and a streaming copy as the practical bandwidth ceiling.  The
 CPU baseline is the repo's multithreaded SIMD CPU encoder (the reference ships
 none) on a bounded sample of the same bytes.
 
@@ -682,6 +682,9 @@ def main() -> int:
     log("encode on a side stream vs bf16 GEMMs")
     over = overlap_with_training(pkg, dev, data, parity, coeff, gemm)
     del gemm
+    torch.cuda.empty_cache()
+    log("training loop with checkpoint saves")
+    over.update(training_with_checkpoints(pkg, dev))
 
     # ---- practical ceiling: the engine's streaming copy (XOR of one shard,
     # same loads/stores as the kernels) and torch's device-to-device copy ---
