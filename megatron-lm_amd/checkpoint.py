@@ -203,8 +203,9 @@ class GpuSliceCodec:
     whole state into one HBM block (288 GB of HBM per MI355X holds a rank's
     (k + m) / k copy) on a stream with its own hardware queue, holds torch's
     stream only for that launch, and stages the block to host memory
-    in a background thread while training goes on.  Transfers use that side
-    stream too, so they never queue behind (or in front of) training work."""
+    in a background thread while training goes on.  Transfers use ordinary
+    streams, where they run on the DMA engines; on the CU-masked side stream
+    they would run as shader copies beside the training kernels."""
 
     def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30,
                  snapshot_bytes: Optional[int] = None):
@@ -309,8 +310,8 @@ class GpuSliceCodec:
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         """Code and stage in bounded chunks; returns when the slices are in
         host memory.  The kernels run on torch's current stream (ordered after
-        the work that produced the tensors), the transfers on the device's
-        side stream."""
+        the work that produced the tensors), the transfers on a stream of
+        torch's pool."""
         from . import _lib
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
