@@ -509,6 +509,8 @@ def training_with_checkpoints(pkg, dev, steps: int = 40, every: int = 10) -> dic
             if save == "sync" and (i + 1) % every == 0:
                 codec.encode(state())
             elif save == "snapshot" and (i + 1) % every == 0:
+                if pending:   # the previous save's slices are written by now: drop
+                    pending.pop().result()   # them, so that their host array is reused
                 pending.append(codec.snapshot(state()))
         torch.cuda.synchronize()
         t = time.perf_counter() - t0
