@@ -209,10 +209,10 @@ int ec_parity_update(const uint8_t* coeff, int k, int m,
  * one after the other.  Measured on MI355X with an 8192^3 bf16 GEMM loop on
  * torch's stream: an RS(6,3) encode beside it on a pooled torch stream slowed
  * the GEMM by 45 % (the two serialized), on this stream by about 1 %, the
- * encode keeping its full rate.  Kernels only: host<->device copies on such
- * a stream run as shader copies on the compute units (on ordinary streams
- * they use the DMA engines) and slowed the kernels beside them up to
- * tenfold in the same measurements.  The mask holds the first n_cus CUs
+ * encode keeping its full rate.  Kernels only: host<->device copies issued
+ * on such a stream held the host and slowed the kernels beside them up to
+ * tenfold in the same measurements (on ordinary streams they did not).  The
+ * mask holds the first n_cus CUs
  * (n_cus <= 0 or at least the device's CU count: all of them; fewer CUs lower
  * the encode's rate in proportion).  *out receives the stream; release it
  * with ec_stream_destroy.  No counterpart in the reference, whose staging
@@ -240,9 +240,9 @@ int ec_stream_destroy(ec_stream_t stream);
  * coded checkpoint in the background while training runs in the same
  * process, whole inside the library (a Python caller through ctypes holds
  * no interpreter lock meanwhile).  Pass an ordinary stream, not one from
- * ec_stream_create: measured on MI355X, transfers on a CU-masked stream run
- * as shader copies on the compute units and slow the kernels beside them,
- * while on an ordinary stream they use the DMA engines. */
+ * ec_stream_create: measured on MI355X, transfers issued on a CU-masked
+ * stream held the host and slowed the kernels beside them; on an ordinary
+ * stream they ran asynchronously without doing so. */
 int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                      uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
                      uint64_t pinned_bytes, int threads, ec_stream_t stream);

@@ -204,8 +204,8 @@ class GpuSliceCodec:
     (k + m) / k copy) on a stream with its own hardware queue, holds torch's
     stream only for that launch, and stages the block to host memory
     in a background thread while training goes on.  Transfers use ordinary
-    streams, where they run on the DMA engines; on the CU-masked side stream
-    they would run as shader copies beside the training kernels."""
+    streams: issued on the CU-masked side stream they held the host and
+    slowed the training kernels beside them."""
 
     def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30,
                  snapshot_bytes: Optional[int] = None):
@@ -323,8 +323,8 @@ class GpuSliceCodec:
         nb = min(2, len(chunks))
         out = self._host_out((k + m, S * U))
         with torch.cuda.device(dev), self._pool() as pool:
-            # transfers on an ordinary stream: they go to the DMA engines (on a
-            # CU-masked stream they ran as shader copies on the compute units)
+            # transfers on an ordinary stream (on the CU-masked side stream they
+            # held the host and slowed the kernels beside them)
             comp, copy = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
             bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
             # per buffer: parity unit (s, i) -> row k + i, data unit (s, p) -> row p
@@ -416,10 +416,9 @@ class GpuSliceCodec:
             out = self._host_out((k + m, S * U))
             pinned = torch.empty(min(2 * self.chunk_bytes, 2 * (k + m) * S * U),
                                  dtype=torch.uint8, pin_memory=True)
-            # The transfers go on an ordinary stream, after the coding: there
-            # they run on the DMA engines, beside training (on the CU-masked
-            # side stream they ran as shader copies and slowed its kernels),
-            # in one foreign call that holds no interpreter lock.
+            # The transfers go on an ordinary stream, after the coding, in one
+            # foreign call that holds no interpreter lock (on the CU-masked
+            # side stream they held the host and slowed training's kernels).
             xfer = torch.cuda.Stream(dev)
             xfer.wait_event(coded)
             block.record_stream(xfer)

@@ -73,8 +73,8 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
     training stream rather than behind it: torch's pooled streams share a few
     hardware queues with the current stream, and work on one queue runs in
     order.  Kernels only: copies between host and device belong on an
-    ordinary stream, where they use the DMA engines (on this CU-masked
-    stream they run as shader copies and slow the kernels beside them).
+    ordinary stream (issued on this CU-masked stream they held the host and
+    slowed the kernels beside them).
     ``cus`` > 0 restricts it to the first ``cus`` CUs.  One stream per
     (device, cus), created on first use and kept for the life of the process
     (the runtime hands out few such queues).  If the runtime refuses one, a

@@ -6,10 +6,9 @@
 // an event wait, host copies on several threads) runs inside one foreign
 // call, which ctypes makes with the interpreter's lock released, so the
 // staging thread takes that lock from the training thread only to start
-// and to finish.  Give it an ordinary stream: on MI355X, transfers on a
-// CU-masked stream ran as shader copies on the compute units and slowed the
-// training kernels beside them, on an ordinary stream they use the DMA
-// engines.
+// and to finish.  Give it an ordinary stream: on MI355X, transfers issued
+// on a CU-masked stream held the host and slowed the training kernels beside
+// them; on ordinary streams they ran asynchronously without doing so.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
