@@ -179,10 +179,11 @@ class GpuSliceCodec:
     zero-padded to ``unit_bytes``): n_stripes * unit_bytes bytes, returned as
     rows of one pageable host array.
 
-    Both directions work in chunks of stripes of at most ``chunk_bytes``,
-    double-buffered on the device and in pinned host memory, so a checkpoint
-    needs 2 * chunk_bytes of extra HBM and of page-locked memory, not
-    (k + m) / k of the state.
+    ``encode`` codes the state into one (k + m) / k block in HBM when that
+    fits (see ``snapshot``) and stages it with ``ec_stage_to_host``;
+    otherwise, and always for ``decode``, the work goes in chunks of stripes
+    of at most ``chunk_bytes``, double-buffered on the device and in pinned
+    host memory: 2 * chunk_bytes of extra HBM and of page-locked memory.
 
     The codec keeps the host array of its last encode and writes the next
     encode of the same shape into it once no slice of it is referenced any
@@ -255,6 +256,16 @@ class GpuSliceCodec:
     def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
         return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
 
+    def _snapshot_limit(self, dev) -> int:
+        """Largest snapshot block: ``snapshot_bytes``, or by default the
+        device's free memory plus what torch's allocator holds unused, less
+        an eighth of the device."""
+        if self.snapshot_bytes is not None:
+            return self.snapshot_bytes
+        free, total = torch.cuda.mem_get_info(dev)
+        idle = torch.cuda.memory_reserved(dev) - torch.cuda.memory_allocated(dev)
+        return free + idle - total // 8
+
     def _meta(self, lay, tensors) -> dict:
         return {"k": self.k, "m": self.m, "unit_bytes": self.unit_bytes,
                 "n_stripes": lay.n_stripes, "n_units": lay.n_units,
@@ -308,6 +319,12 @@ class GpuSliceCodec:
         return ThreadPoolExecutor(max_workers=_COPY_THREADS)
 
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
+        """Code the tensors into k + m slices in host memory; returns when
+        they are there.  Through one HBM block when it fits (``snapshot``,
+        waited for), else in bounded chunks: the same slices either way."""
+        return self.snapshot(tensors).result()
+
+    def _encode_chunked(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         """Code and stage in bounded chunks; returns when the slices are in
         host memory.  The kernels run on torch's current stream (ordered after
         the work that produced the tensors), the transfers on a stream of
@@ -369,10 +386,12 @@ class GpuSliceCodec:
         would.  Without ``hold`` the caller must order its own writes after
         ``PendingSlices.coded``.
 
-        When the block is larger than ``snapshot_bytes`` or the allocator
-        cannot provide it, the state is coded and staged by ``encode`` before
-        this returns (the bounded chunked path: a longer stall, the same
-        slices), and the result is ready at once."""
+        When the block is larger than ``snapshot_bytes`` (by default: than
+        what leaves an eighth of the device's memory free, so that the next
+        training steps keep their room) or the allocator cannot provide it,
+        the state is coded and staged by ``encode`` before this returns (the
+        bounded chunked path: a longer stall, the same slices), and the
+        result is ready at once."""
         from . import _lib
         from .codec import side_stream, stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
@@ -381,14 +400,14 @@ class GpuSliceCodec:
         S, dev = lay.n_stripes, lay.device
         cur = torch.cuda.current_stream(dev)
         block = None
-        if self.snapshot_bytes is None or (k + m) * S * U <= self.snapshot_bytes:
+        if (k + m) * S * U <= self._snapshot_limit(dev):
             try:
                 with torch.cuda.device(dev):
                     block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
             except torch.OutOfMemoryError:
                 block = None
         if block is None:
-            ready = self.encode(tensors)
+            ready = self._encode_chunked(tensors)
             coded = torch.cuda.Event()
             coded.record(cur)
             return PendingSlices(coded, ready=ready)

@@ -18,10 +18,12 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("k,m,unit", [(4, 2, 1024), (6, 3, 4096), (2, 1, 256), (12, 4, 65536)])
 @pytest.mark.parametrize("chunk_stripes", [None, 3])
 def test_gpu_slices_match_oracle_and_decode(pkg, dev, k, m, unit, chunk_stripes):
-    """chunk_stripes = 3: device staging in chunks of about 3 stripes, so
-    both buffers are reused and the last chunk is partial."""
+    """chunk_stripes = None: the one-block path; 3: the chunked path with
+    chunks of about 3 stripes, so both buffers are reused and the last chunk
+    is partial."""
     from megatron_lm_amd.checkpoint import GpuSliceCodec
-    kw = {} if chunk_stripes is None else {"chunk_bytes": chunk_stripes * (k + m) * unit}
+    kw = {} if chunk_stripes is None else {"chunk_bytes": chunk_stripes * (k + m) * unit,
+                                           "snapshot_bytes": 0}
     cpu = make_tensors(3) + make_tensors(2)
     gpu = [t.to(dev) for t in cpu]
     gmeta, gs = GpuSliceCodec(k, m, unit, **kw).encode(gpu)
