@@ -207,8 +207,9 @@ int ec_parity_update(const uint8_t* coeff, int k, int m,
  * HIP runtime, while plain streams (torch's pooled ones among them) share at
  * most GPU_MAX_HW_QUEUES queues round robin, and two streams on one queue run
  * one after the other.  Measured on MI355X with an 8192^3 bf16 GEMM loop on
- * torch's stream: an RS(6,3) encode beside it on a pooled torch stream slowed
- * the GEMM by 45 % (the two serialized), on this stream by about 1 %, the
+ * torch's stream: an RS(6,3) encode beside it on a pooled torch stream that
+ * had landed on torch's queue slowed the GEMM by 45 % (the two serialized),
+ * on this stream by about 1 %, the
  * encode keeping its full rate.  Kernels only: host<->device copies issued
  * on such a stream held the host and slowed the kernels beside them up to
  * tenfold in the same measurements (on ordinary streams they did not).  The
