@@ -438,13 +438,14 @@ class GpuSliceCodec:
             # The transfers go on an ordinary stream, after the coding, in one
             # foreign call that holds no interpreter lock (on the CU-masked
             # side stream they held the host and slowed training's kernels).
-            xfer = torch.cuda.Stream(dev)
-            xfer.wait_event(coded)
-            block.record_stream(xfer)
-            _lib.check(_lib.lib().ec_stage_to_host(
-                block.data_ptr(), S * U, out.ctypes.data, S * U, k + m, S * U,
-                pinned.data_ptr(), pinned.numel(), self.stage_threads,
-                stream_handle(xfer, dev)), "ec_stage_to_host")
+            with torch.cuda.device(dev):
+                xfer = torch.cuda.Stream(dev)
+                xfer.wait_event(coded)
+                block.record_stream(xfer)
+                _lib.check(_lib.lib().ec_stage_to_host(
+                    block.data_ptr(), S * U, out.ctypes.data, S * U, k + m, S * U,
+                    pinned.data_ptr(), pinned.numel(), self.stage_threads,
+                    stream_handle(xfer, dev)), "ec_stage_to_host")
             block = None   # back to the allocator: the last transfer has landed
             return meta, [out[p] for p in range(k + m)]
 

@@ -61,6 +61,14 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
   if (width == 0) return EC_EINVAL;
   width = std::min(width, row_bytes);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // The events belong on the stream's device, whichever device the calling
+  // thread has current.
+  int prev = 0;
+  hipDevice_t sdev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
+  if (st && hipStreamGetDevice(st, &sdev) != hipSuccess) return EC_EHIP;
+  const bool switched = st && sdev != prev;
+  if (switched && hipSetDevice(sdev) != hipSuccess) return EC_EHIP;
   hipEvent_t ev[2] = {nullptr, nullptr};
   int status = EC_OK;
   for (auto& e : ev)
@@ -92,6 +100,7 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
   if (status != EC_OK) (void)hipStreamSynchronize(st);  // no transfer outlives the call
   for (auto& e : ev)
     if (e) (void)hipEventDestroy(e);
+  if (switched) (void)hipSetDevice(prev);
   return status;
 }
 
