@@ -120,3 +120,31 @@ def test_row_addresses_on_device_match_host():
                         axis=1).view(np.int64)
         got = ck.GpuSliceCodec._row_ptrs(block, first, count).numpy()
         assert np.array_equal(got, want), (first, count)
+
+
+def test_copy_rows_over_a_pool():
+    """The blocking paths' host copies: every row lands whole, whatever the
+    row count against the pool's threads."""
+    from concurrent.futures import ThreadPoolExecutor
+    rng = np.random.default_rng(3)
+    with ThreadPoolExecutor(max_workers=4) as pool:
+        for rows in (1, 3, 16, 17):
+            src = rng.integers(0, 256, (rows, 1000), dtype=np.uint8)
+            dst = np.zeros((rows, 1000), np.uint8)
+            for f in ck._copy_rows(pool, dst, lambda r: src[r]):
+                f.result()
+            assert np.array_equal(dst, src), rows
+
+
+def test_await_marker(tmp_path):
+    """async_fn of a background save: returns once the marker exists, raises
+    TimeoutError when it never comes."""
+    import threading
+    import time
+    marker = tmp_path / ".iter_0000001.staged"
+    threading.Timer(0.1, lambda: marker.write_text("ok")).start()
+    t0 = time.monotonic()
+    ck._await_marker(str(marker), timeout=10)
+    assert time.monotonic() - t0 < 5
+    with pytest.raises(TimeoutError):
+        ck._await_marker(str(tmp_path / "never"), timeout=0.05)
