@@ -3,7 +3,10 @@
  * binding (cgo, JNI, N-API) would use it: device buffers from hipMalloc, an
  * explicit stream, status codes.  Encodes RS(6,3) over 6 shards, loses 3
  * seeded shards, reconstructs them and checks them byte for byte; does the
- * same for XOR parity.  Prints "ec_abi_demo ok" and exits 0 on success.
+ * same for XOR parity; then codes the shards as one stripe into a snapshot
+ * block (ec_encode_batched_copy) and stages the block to host memory
+ * (ec_stage_to_host), as a background checkpoint save does, checking every
+ * row.  Prints "ec_abi_demo ok" and exits 0 on success.
  *
  *   ec_abi_demo [shard_bytes]
  */
@@ -98,6 +101,59 @@ int main(int argc, char** argv) {
       return 1;
     }
   }
+  /* a checkpoint snapshot: the 6 shards as the units of one stripe, coded
+   * into a (6 + 3) x unit block in one pass, then staged to host memory on an
+   * ordinary stream through a pinned buffer */
+  {
+    const uint64_t unit = (n + 15) & ~(uint64_t)15;
+    if (unit > (1ull << 31)) return 6;
+    uint8_t* block;
+    CHECK_HIP(hipMalloc((void**)&block, (K + M) * unit));
+    uint64_t h_desc[K + M + K];
+    uint32_t h_len[K];
+    for (int j = 0; j < K; ++j) {
+      h_desc[j] = (uint64_t)(uintptr_t)dev[j];                    /* units */
+      h_desc[K + M + j] = (uint64_t)(uintptr_t)(block + j * unit);  /* copies */
+      h_len[j] = (uint32_t)n;
+    }
+    for (int i = 0; i < M; ++i) h_desc[K + i] = (uint64_t)(uintptr_t)(block + (K + i) * unit);
+    uint64_t* d_desc;
+    uint32_t* d_len;
+    CHECK_HIP(hipMalloc((void**)&d_desc, sizeof h_desc));
+    CHECK_HIP(hipMalloc((void**)&d_len, sizeof h_len));
+    CHECK_HIP(hipMemcpy(d_desc, h_desc, sizeof h_desc, hipMemcpyHostToDevice));
+    CHECK_HIP(hipMemcpy(d_len, h_len, sizeof h_len, hipMemcpyHostToDevice));
+    CHECK_EC(ec_encode_batched_copy(coeff, K, M, d_desc, d_len, d_desc + K, d_desc + K + M, 1,
+                                    (uint32_t)unit, st));
+    CHECK_HIP(hipStreamSynchronize((hipStream_t)st));
+    hipStream_t xfer;
+    CHECK_HIP(hipStreamCreate(&xfer));
+    const uint64_t pinned_bytes = 1u << 24; /* smaller than the block for large shards */
+    uint8_t* pinned;
+    CHECK_HIP(hipHostMalloc((void**)&pinned, pinned_bytes, hipHostMallocDefault));
+    uint8_t* slices = (uint8_t*)malloc((K + M) * unit);
+    CHECK_EC(ec_stage_to_host(block, unit, slices, unit, K + M, unit, pinned, pinned_bytes, 4,
+                              (ec_stream_t)xfer));
+    for (int g = 0; g < K + M; ++g) {
+      const uint8_t* row = slices + g * unit;
+      if (memcmp(row, host[g], n) != 0) {
+        fprintf(stderr, "snapshot row %d differs\n", g);
+        return 1;
+      }
+      for (uint64_t b = n; b < unit; ++b)
+        if (row[b] != 0) {
+          fprintf(stderr, "snapshot row %d not zero-padded\n", g);
+          return 1;
+        }
+    }
+    free(slices);
+    CHECK_HIP(hipHostFree(pinned));
+    CHECK_HIP(hipStreamDestroy(xfer));
+    CHECK_HIP(hipFree(d_desc));
+    CHECK_HIP(hipFree(d_len));
+    CHECK_HIP(hipFree(block));
+  }
+
   /* too many erasures is an error, not a crash */
   const int four[4] = {0, 1, 2, 3};
   if (ec_decode_matrix(coeff, K, M, four, 4, surv, rows) != EC_ESINGULAR) return 5;

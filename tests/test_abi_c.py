@@ -1,5 +1,6 @@
 """The C ABI from C: the header is strict C, and a plain-C program linked
-against libec_mi355.so encodes, reconstructs and XORs on the GPU."""
+against libec_mi355.so encodes, reconstructs and XORs on the GPU, and codes a
+checkpoint snapshot and stages it to host memory."""
 import os
 import subprocess
 
