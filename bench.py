@@ -211,6 +211,8 @@ def checkpoint_staging(pkg, tensors) -> dict:
                 raise AssertionError("checkpoint decode did not rebuild the tensors")
             del rebuilt
         del keep
+        log(f"staging calls: encode {[round(t, 3) for t in t_enc]} s (cold {t_cold:.3f}), "
+            f"decode {[round(t, 3) for t in t_dec]} s")
         res = {"ckpt_encode_to_host_GBps": round(nbytes / statistics.median(t_enc) / 1e9, 1),
                "ckpt_encode_to_host_cold_GBps": round(nbytes / t_cold / 1e9, 1),
                "ckpt_decode_from_host_GBps": round(nbytes / statistics.median(t_dec) / 1e9, 1)}

@@ -248,6 +248,21 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                      uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
                      uint64_t pinned_bytes, int threads, ec_stream_t stream);
 
+/* The way back: row r of a rows x row_bytes region, read from the host
+ * array h_rows[r] (need not be pinned; a host array of row_bytes bytes
+ * each), goes to d_dst + r * dst_pitch in device memory, through the
+ * caller's pinned buffer (two halves: `threads` host threads fill one while
+ * the other's transfer runs on `stream`).  Returns when every byte is in
+ * device memory; the transfers follow the work already enqueued on
+ * `stream`.  Same argument rules as ec_stage_to_host (and null rows are
+ * EC_EINVAL).  No counterpart in the reference: its H2D is
+ * restore_tensor_device (tensor_aware_state_dict.py:245-274); this call
+ * brings the k slices a rank read back into HBM for the decode of
+ * manager.load (checkpointing.py:891-894). */
+int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row_bytes,
+                       uint8_t* d_dst, uint64_t dst_pitch, uint8_t* h_pinned,
+                       uint64_t pinned_bytes, int threads, ec_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

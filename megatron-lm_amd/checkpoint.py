@@ -181,9 +181,11 @@ class GpuSliceCodec:
 
     ``encode`` codes the state into one (k + m) / k block in HBM when that
     fits (see ``snapshot``) and stages it with ``ec_stage_to_host``;
-    otherwise, and always for ``decode``, the work goes in chunks of stripes
-    of at most ``chunk_bytes``, double-buffered on the device and in pinned
-    host memory: 2 * chunk_bytes of extra HBM and of page-locked memory.
+    otherwise the work goes in chunks of stripes of at most ``chunk_bytes``,
+    double-buffered on the device and in pinned host memory: 2 * chunk_bytes
+    of extra HBM and of page-locked memory.  ``decode`` likewise takes one
+    (k, stripes, unit_bytes) block when it fits, else chunks, and moves the
+    slices up with ``ec_stage_to_device``.
 
     The codec keeps the host array of its last encode and writes the next
     encode of the same shape into it once no slice of it is referenced any
@@ -195,10 +197,10 @@ class GpuSliceCodec:
     buffer's parity rows and, in the same pass over the data, the data units
     (zero-padded) into its data rows; the buffer goes to pinned memory on a
     copy stream, and four threads move it into the result while the next
-    chunk is coded and transferred.  Decode, per chunk: the threads copy the
-    k slices' part into pinned memory, the copy stream sends it up, one scatter
+    chunk is coded and transferred.  Decode, per chunk (one, when the block
+    fits): ``ec_stage_to_device`` moves the k slices' part up, one scatter
     launch puts the data rows into fresh tensors and one decode launch
-    rebuilds the lost data positions; the next chunk's host copy overlaps.
+    rebuilds the lost data positions.
 
     ``snapshot`` is the save path that keeps training running: it codes the
     whole state into one HBM block (288 GB of HBM per MI355X holds a rank's
@@ -475,18 +477,29 @@ class GpuSliceCodec:
             if surv != avail:
                 raise CheckpointingException("decode plan does not match the slices read")
             rows = np.ascontiguousarray(rows[[erased.index(p) for p in lost_data]])
-        C = self._chunk_stripes(S, k)
-        chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
-        nb = min(2, len(chunks))
+        # One chunk when the (k, S, U) block fits beside training (the bound of
+        # snapshot), else chunks of at most chunk_bytes, double-buffered.
+        C = S if k * S * U <= self._snapshot_limit(device) else self._chunk_stripes(S, k)
         one = np.ones((1, 1), np.uint8)
         hp = [p for _, p in have]
-        with torch.cuda.device(device), self._pool() as pool:
+        src = [np.ascontiguousarray(slices[p]).reshape(-1) for p in avail]
+        with torch.cuda.device(device):
             comp, copy = torch.cuda.current_stream(device), torch.cuda.Stream(device)
-            bufs = [torch.empty((k, C, U), dtype=torch.uint8, device=device) for _ in range(nb)]
+            while True:
+                chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
+                nb = min(2, len(chunks))
+                try:
+                    bufs = [torch.empty((k, C, U), dtype=torch.uint8, device=device)
+                            for _ in range(nb)]
+                    break
+                except torch.OutOfMemoryError:
+                    if C == self._chunk_stripes(S, k):
+                        raise
+                    C = self._chunk_stripes(S, k)
             for bf in bufs:
                 bf.record_stream(copy)
-            pins = [torch.empty((k, C, U), dtype=torch.uint8, pin_memory=True)
-                    for _ in range(nb)]
+            pinned = torch.empty(min(2 * self.chunk_bytes, 2 * k * C * U), dtype=torch.uint8,
+                                 pin_memory=True)
             # Every descriptor array is uploaded once, stripe-major, so that a
             # chunk's descriptors are a contiguous slice (a pointer offset).
             full = torch.full((C * k,), U, dtype=torch.int32, device=device)
@@ -499,27 +512,19 @@ class GpuSliceCodec:
                                  np.int64, device) for bf in bufs]
             dec_dst = self._dev(lay.host_ptrs[:, lost_data], np.int64, device)
             dec_len = self._dev(lay.host_len[:, lost_data], np.int32, device)
-            sent: List[torch.cuda.Event] = []      # chunk n has left pins[n % nb]
             consumed: List[torch.cuda.Event] = []  # chunk n is decoded out of bufs[n % nb]
-
-            def fill(n):
-                c0, c = chunks[n]
-                return _copy_rows(pool, pins[n % nb].numpy()[:, :c].reshape(k, -1),
-                                  lambda r: slices[avail[r]][c0 * U:(c0 + c) * U])
-
-            filling = fill(0)
             for n, (c0, c) in enumerate(chunks):
                 b = n % nb
-                for f in filling:
-                    f.result()
                 if n >= nb:
                     copy.wait_event(consumed[n - nb])  # device buffer b is free again
-                with torch.cuda.stream(copy):  # row by row: each row's part is contiguous
-                    for r in range(k):
-                        bufs[b][r, :c].copy_(pins[b][r, :c], non_blocking=True)
-                sent.append(torch.cuda.Event())
-                sent[-1].record(copy)
-                comp.wait_event(sent[-1])
+                # the k slices' part of the chunk into the buffer's rows, in one
+                # native call (host threads fill pinned halves, the copy stream
+                # sends them up); it returns once the bytes are on the device
+                _lib.check(_lib.lib().ec_stage_to_device(
+                    _lib.ptr_array([a.ctypes.data + c0 * U for a in src]), k, c * U,
+                    bufs[b].data_ptr(), C * U, pinned.data_ptr(), pinned.numel(),
+                    self.stage_threads, stream_handle(copy, device)), "ec_stage_to_device")
+                comp.wait_stream(copy)
                 if have:  # the data slices we have go into the tensors
                     h = len(have)
                     _lib.check(_lib.lib().ec_decode_batched(
@@ -534,10 +539,6 @@ class GpuSliceCodec:
                         c, U, stream_handle(comp, device)), "ec_decode_batched")
                 consumed.append(torch.cuda.Event())
                 consumed[-1].record(comp)
-                if n + 1 < len(chunks):
-                    if n + 1 >= nb:
-                        sent[n + 1 - nb].synchronize()  # pinned buffer is free again
-                    filling = fill(n + 1)               # overlaps chunk n's transfer
             comp.synchronize()
         return tensors
 

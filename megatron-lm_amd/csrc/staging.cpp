@@ -1,5 +1,5 @@
 // staging.cpp — host side of moving coded checkpoint slices out of HBM
-// (ec_stage_to_host).
+// (ec_stage_to_host) and back in (ec_stage_to_device).
 //
 // A background save stages the coded block to host memory while training
 // runs in the same process.  The whole loop (a transfer per chunk and row,
@@ -98,6 +98,70 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
     }
   }
   if (status != EC_OK) (void)hipStreamSynchronize(st);  // no transfer outlives the call
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  if (switched) (void)hipSetDevice(prev);
+  return status;
+}
+
+int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row_bytes,
+                       uint8_t* d_dst, uint64_t dst_pitch, uint8_t* h_pinned,
+                       uint64_t pinned_bytes, int threads, ec_stream_t stream) {
+  if (rows == 0 || row_bytes == 0) return EC_OK;
+  if (!h_rows || !d_dst || !h_pinned || threads < 1 || threads > 64) return EC_EINVAL;
+  for (uint32_t r = 0; r < rows; ++r)
+    if (!h_rows[r]) return EC_EINVAL;
+  if (dst_pitch < row_bytes) return EC_EINVAL;
+  const uint64_t half = pinned_bytes / 2;
+  uint64_t width = half / rows;
+  if (width >= 4096) width -= width % 4096;
+  if (width == 0) return EC_EINVAL;
+  width = std::min(width, row_bytes);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int prev = 0;
+  hipDevice_t sdev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
+  if (st && hipStreamGetDevice(st, &sdev) != hipSuccess) return EC_EHIP;
+  const bool switched = st && sdev != prev;
+  if (switched && hipSetDevice(sdev) != hipSuccess) return EC_EHIP;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  int status = EC_OK;
+  for (auto& e : ev)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
+      status = EC_EHIP;
+  const uint64_t n_chunks = (row_bytes + width - 1) / width;
+  // Chunk j: the threads fill pinned half j % 2 (once the transfer of chunk
+  // j - 2 out of it has landed), then the transfer is enqueued; the fill of
+  // chunk j + 1 overlaps it.
+  for (uint64_t j = 0; status == EC_OK && j < n_chunks; ++j) {
+    const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
+    uint8_t* pin = h_pinned + (j % 2) * half;
+    if (j >= 2 && hipEventSynchronize(ev[j % 2]) != hipSuccess) {
+      status = EC_EHIP;
+      break;
+    }
+    // rows x w bytes, split over the threads by equal shares of bytes
+    const uint64_t total = (uint64_t)rows * w, share = (total + threads - 1) / threads;
+    auto run = [&](int t) {
+      uint64_t b = (uint64_t)t * share, e = std::min(total, b + share);
+      while (b < e) {
+        const uint64_t r = b / w, x = b % w, n = std::min(e - b, w - x);
+        memcpy(pin + r * w + x, h_rows[r] + x0 + x, n);
+        b += n;
+      }
+    };
+    std::vector<std::thread> pool;
+    for (int t = 1; t < threads; ++t) pool.emplace_back(run, t);
+    run(0);
+    for (auto& th : pool) th.join();
+    for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
+      if (hipMemcpyAsync(d_dst + (uint64_t)r * dst_pitch + x0, pin + (uint64_t)r * w, w,
+                         hipMemcpyHostToDevice, st) != hipSuccess)
+        status = EC_EHIP;
+    if (status == EC_OK && hipEventRecord(ev[j % 2], st) != hipSuccess) status = EC_EHIP;
+  }
+  // no transfer outlives the call: the pinned buffer is the caller's again
+  if (hipStreamSynchronize(st) != hipSuccess && status == EC_OK) status = EC_EHIP;
   for (auto& e : ev)
     if (e) (void)hipEventDestroy(e);
   if (switched) (void)hipSetDevice(prev);

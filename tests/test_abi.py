@@ -136,3 +136,19 @@ def test_stage_to_host_rejects_bad_arguments(pkg):
     assert L.ec_stage_to_host(p, 64, p, 64, 2, 64, p, 256, 0, None) == pkg._lib.EC_EINVAL
     assert L.ec_stage_to_host(p, 64, p, 64, 2, 64, p, 256, 65, None) == pkg._lib.EC_EINVAL
     assert L.ec_stage_to_host(p, 64, p, 64, 4, 64, p, 6, 4, None) == pkg._lib.EC_EINVAL
+
+
+def test_stage_to_device_rejects_bad_arguments(pkg):
+    """Host-side validation of ec_stage_to_device (no device work)."""
+    L = pkg._lib.lib()
+    p = ctypes.c_void_p(4096)
+    rows = (ctypes.c_void_p * 2)(4096, 8192)
+    hole = (ctypes.c_void_p * 2)(4096, None)
+    assert L.ec_stage_to_device(rows, 0, 64, p, 64, p, 256, 4, None) == pkg._lib.EC_OK
+    assert L.ec_stage_to_device(rows, 2, 0, p, 64, p, 256, 4, None) == pkg._lib.EC_OK
+    assert L.ec_stage_to_device(None, 2, 64, p, 64, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_device(hole, 2, 64, p, 64, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_device(rows, 2, 64, None, 64, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_device(rows, 2, 64, p, 32, p, 256, 4, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_device(rows, 2, 64, p, 64, p, 256, 0, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_to_device(rows, 2, 64, p, 64, p, 2, 4, None) == pkg._lib.EC_EINVAL

@@ -571,3 +571,26 @@ def test_stage_to_host(pkg, dev, rows, row_bytes, pitch, pinned, threads):
     want = src.cpu().numpy()
     assert np.array_equal(out[:, :row_bytes], want[:, :row_bytes])
     assert (out[:, row_bytes:] == 0x77).all()
+
+
+@pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [
+    (12, (1 << 20) + 48, (1 << 20) + 64, 1 << 20, 8),
+    (3, 5000, 5008, 64, 1),
+    (1, 4096, 8192, 1 << 16, 64),
+])
+def test_stage_to_device(pkg, dev, rows, row_bytes, pitch, pinned, threads):
+    """ec_stage_to_device copies separate pageable host rows into a pitched
+    device region exactly, through a pinned buffer smaller than the region,
+    and leaves the bytes between rows alone."""
+    from megatron_lm_amd import _lib
+    rng = np.random.default_rng(rows)
+    host = [rng.integers(0, 256, row_bytes, dtype=np.uint8) for _ in range(rows)]
+    dst = torch.full((rows, pitch), 0x5A, dtype=torch.uint8, device=dev)
+    pin = torch.empty(pinned, dtype=torch.uint8, pin_memory=True)
+    _lib.check(_lib.lib().ec_stage_to_device(
+        _lib.ptr_array([h.ctypes.data for h in host]), rows, row_bytes, dst.data_ptr(), pitch,
+        pin.data_ptr(), pinned, threads, None), "ec_stage_to_device")
+    got = dst.cpu().numpy()
+    for r in range(rows):
+        assert np.array_equal(got[r, :row_bytes], host[r]), r
+        assert (got[r, row_bytes:] == 0x5A).all(), r
