@@ -21,6 +21,24 @@
 
 namespace {
 
+// run(t) for t in [0, threads), share 0 on the calling thread and the others
+// on threads of their own.  A thread that cannot be started (the system is
+// out of threads or memory) has its share run on the calling thread, so no
+// C++ exception reaches the C ABI and every started thread is joined.
+template <class F>
+void run_shares(int threads, const F& run) {
+  std::vector<std::thread> pool;
+  int t = 1;
+  try {
+    pool.reserve(threads - 1);
+    for (; t < threads; ++t) pool.emplace_back(run, t);
+  } catch (...) {
+  }
+  for (int u = t; u < threads; ++u) run(u);
+  run(0);
+  for (auto& th : pool) th.join();
+}
+
 // dst[r * dst_pitch + x] = src[r * src_pitch + x] for r < rows, x < width,
 // split by rows (or by column ranges when rows < threads) over `threads`
 // host threads.
@@ -38,10 +56,7 @@ void copy_rect(uint8_t* dst, uint64_t dst_pitch, const uint8_t* src, uint64_t sr
       begin += n;
     }
   };
-  std::vector<std::thread> pool;
-  for (int t = 1; t < threads; ++t) pool.emplace_back(run, t);
-  run(0);
-  for (auto& th : pool) th.join();
+  run_shares(threads, run);
 }
 
 }  // namespace
@@ -150,10 +165,7 @@ int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row
         b += n;
       }
     };
-    std::vector<std::thread> pool;
-    for (int t = 1; t < threads; ++t) pool.emplace_back(run, t);
-    run(0);
-    for (auto& th : pool) th.join();
+    run_shares(threads, run);
     for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
       if (hipMemcpyAsync(d_dst + (uint64_t)r * dst_pitch + x0, pin + (uint64_t)r * w, w,
                          hipMemcpyHostToDevice, st) != hipSuccess)
