@@ -23,32 +23,54 @@ from . import _lib
 from .codec import _dev, cauchy_matrix, decode_matrix, stream_handle
 
 
-def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
+def stripe_descriptors(base: np.ndarray, size: np.ndarray, k: int,
+                       unit_bytes: int) -> Tuple[int, np.ndarray, np.ndarray]:
     """Cut tensors (device base addresses ``base``, byte sizes ``size``), in
     order, into units of ``unit_bytes`` and group them into stripes of k.
+    Returns (n_units, ptrs, lens): [n_stripes, k] arrays of unit addresses
+    (0 = absent slot of the last stripe) and valid lengths.  Zero-byte
+    tensors contribute no unit; an empty list gives one empty stripe.
 
-    Returns (unit_tensor, unit_index, ptrs, lens): for each unit its tensor
-    and its index inside that tensor, and [n_stripes, k] arrays of unit
-    addresses (0 = absent slot of the last stripe) and valid lengths.
-    Zero-byte tensors contribute no unit; an empty list gives one empty
-    stripe."""
+    Unit u of the flat order belongs to tensor t with first[t] <= u <
+    first[t] + n[t] (first = exclusive prefix sum of the unit counts n), so
+    its address is (base[t] - first[t] * unit_bytes) + u * unit_bytes, and
+    every unit is full except each tensor's last: the work per unit is one
+    multiply-add, the rest is per tensor (a save codes ~3,000 tensors cut
+    into ~300,000 units, on the path that holds training)."""
     base = np.asarray(base, np.uint64).reshape(-1)
     size = np.asarray(size, np.int64).reshape(-1)
-    if size.size == 0:
-        empty = np.zeros(0, np.int64)
-        return empty, empty, np.zeros((1, k), np.uint64), np.zeros((1, k), np.uint32)
-    n_units = (size + unit_bytes - 1) // unit_bytes
-    unit_tensor = np.repeat(np.arange(size.size), n_units)
-    first = np.concatenate([[0], np.cumsum(n_units)[:-1]]).astype(np.int64)
-    unit_index = np.arange(unit_tensor.size) - np.repeat(first, n_units)
-    total = int(unit_tensor.size)
+    n = (size + unit_bytes - 1) // unit_bytes
+    total = int(n.sum())
     n_stripes = max(1, (total + k - 1) // k)
     ptr = np.zeros(n_stripes * k, np.uint64)
     ln = np.zeros(n_stripes * k, np.uint32)
-    off = unit_index.astype(np.uint64) * np.uint64(unit_bytes)
-    ptr[:total] = base[unit_tensor] + off
-    ln[:total] = np.minimum(size[unit_tensor] - off.astype(np.int64), unit_bytes).astype(np.uint32)
-    return unit_tensor, unit_index, ptr.reshape(n_stripes, k), ln.reshape(n_stripes, k)
+    if total:
+        first = np.cumsum(n) - n
+        addr = np.arange(total, dtype=np.int64)
+        addr *= unit_bytes
+        addr += np.repeat(base.view(np.int64) - first * unit_bytes, n)
+        ptr[:total] = addr.view(np.uint64)
+        ln[:total] = unit_bytes
+        has = n > 0
+        ln[(first + n - 1)[has]] = (size - (n - 1) * unit_bytes)[has]
+    return total, ptr.reshape(n_stripes, k), ln.reshape(n_stripes, k)
+
+
+def unit_owners(size: np.ndarray, unit_bytes: int) -> Tuple[np.ndarray, np.ndarray]:
+    """(unit_tensor, unit_index) of the flat unit order of ``stripe_descriptors``:
+    each unit's tensor and its index inside that tensor."""
+    size = np.asarray(size, np.int64).reshape(-1)
+    n = (size + unit_bytes - 1) // unit_bytes
+    unit_tensor = np.repeat(np.arange(size.size), n)
+    unit_index = np.arange(unit_tensor.size) - np.repeat(np.cumsum(n) - n, n)
+    return unit_tensor, unit_index
+
+
+def unit_table(base: np.ndarray, size: np.ndarray, k: int, unit_bytes: int):
+    """(unit_tensor, unit_index, ptrs, lens): ``unit_owners`` and
+    ``stripe_descriptors`` together."""
+    _, ptr, ln = stripe_descriptors(base, size, k, unit_bytes)
+    return (*unit_owners(size, unit_bytes), ptr, ln)
 
 
 def _upload(a: np.ndarray, device) -> torch.Tensor:
@@ -119,9 +141,9 @@ class StripeLayout:
                 torch.device("cuda", torch.cuda.current_device())
         base, size = _spans(self.tensors, self.device)
         self.tensor_bytes = size
-        (self.unit_tensor, self.unit_index, self.host_ptrs,
-         self.host_len) = unit_table(base, size, k, unit_bytes)
-        self.n_units = int(self.unit_tensor.size)
+        self.n_units, self.host_ptrs, self.host_len = stripe_descriptors(base, size, k,
+                                                                         unit_bytes)
+        self._owners = None
         self.n_stripes = self.host_ptrs.shape[0]
         self.data_bytes = int(size.sum())
         # Through pinned memory, asynchronously on the device's current stream:
@@ -132,6 +154,20 @@ class StripeLayout:
             self.d_len = _upload(self.host_len.view(np.int32), self.device)
             self.uploaded = torch.cuda.Event()
             self.uploaded.record()
+
+    @property
+    def unit_tensor(self) -> np.ndarray:
+        """Tensor of each unit, in the flat unit order (built on first use)."""
+        if self._owners is None:
+            self._owners = unit_owners(self.tensor_bytes, self.unit_bytes)
+        return self._owners[0]
+
+    @property
+    def unit_index(self) -> np.ndarray:
+        """Index of each unit inside its tensor (built on first use)."""
+        if self._owners is None:
+            self._owners = unit_owners(self.tensor_bytes, self.unit_bytes)
+        return self._owners[1]
 
     # ------------------------------------------------------------ parity --
 

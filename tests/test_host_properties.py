@@ -12,7 +12,7 @@ from test_layout_cpu import loop_layout
 
 ec = __graft_entry__.load_package()
 from megatron_lm_amd import checkpoint as ck  # noqa: E402
-from megatron_lm_amd.layout import unit_table  # noqa: E402
+from megatron_lm_amd.layout import stripe_descriptors, unit_table  # noqa: E402
 
 
 @settings(max_examples=80, deadline=None, suppress_health_check=[HealthCheck.too_slow])
@@ -30,6 +30,7 @@ def test_unit_table_random(k, unit16, seed, n):
     assert np.array_equal(owner, o2) and np.array_equal(P, P2) and np.array_equal(L, L2)
     assert int(L.sum()) == int(size.sum())
     assert P.shape[0] == max(1, -(-owner.size // k))
+    assert stripe_descriptors(base, size, k, unit)[0] == owner.size
     # absent slots of the last stripe are (0, 0); present units are non-empty
     flat_l, flat_p = L.reshape(-1), P.reshape(-1)
     assert (flat_l[: owner.size] > 0).all() and not flat_l[owner.size:].any()
