@@ -117,8 +117,9 @@ _staging_join_registered = False
 
 
 def _join_staging_threads() -> None:
-    """At interpreter exit: let background staging finish before the side
-    streams it uses are destroyed (registered after them, so it runs first)."""
+    """At interpreter exit: let background staging finish before the hook
+    that waits for the side streams (registered after it, so it runs
+    first)."""
     for t in list(_staging_threads):
         t.join()
 

@@ -56,15 +56,16 @@ _side: Dict[Tuple[int, int], torch.cuda.ExternalStream] = {}
 _side_lock = threading.Lock()
 
 
-def _release_side_streams() -> None:
-    """At interpreter exit: finish and destroy the streams of
-    ``side_stream`` while the HIP runtime is still whole."""
+def _finish_side_streams() -> None:
+    """At interpreter exit: let the work on the streams of ``side_stream``
+    finish.  The streams themselves are never destroyed here: tensors that
+    outlive this hook (module globals, freed after it) may carry
+    ``record_stream`` uses of them, and the caching allocator records an
+    event on each such stream when it frees them; the end of the process
+    releases the streams with the rest of the HIP context."""
     with _side_lock:
         for s in _side.values():
-            if isinstance(s, torch.cuda.ExternalStream):
-                s.synchronize()
-                _lib.lib().ec_stream_destroy(ctypes.c_void_p(s.cuda_stream))
-        _side.clear()
+            s.synchronize()
 
 
 def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
@@ -92,7 +93,7 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
             status = _lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h))
             if status == _lib.EC_OK:
                 if not _side:
-                    atexit.register(_release_side_streams)
+                    atexit.register(_finish_side_streams)
                 s = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
             else:  # the kernels still run; only the overlap with training is lost
                 warnings.warn(f"ec_stream_create on device {idx}: {_lib.strerror(status)}; "

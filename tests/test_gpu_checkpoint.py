@@ -3,11 +3,14 @@ byte-identical to the oracle codec's, every k-subset of slices decodes, and
 the multi-rank recovery scenario runs with ranks sharing the GPU (gloo for
 the exchange, CPU tensors on the wire)."""
 import itertools
+import subprocess
+import sys
 
 import numpy as np
 import pytest
 import torch
 
+from conftest import ROOT
 from ec_cpu_codec import OracleSliceCodec
 from ec_ckpt_worker import bump, make_tensors, same
 from test_checkpoint_cpu import launch
@@ -171,3 +174,27 @@ def test_gpu_snapshot_falls_back_to_chunks(pkg, dev):
     meta, slices = pending.result(timeout=60)
     ometa, oslices = OracleSliceCodec(4, 2, 1024).encode(cpu)
     assert meta == ometa and all(np.array_equal(a, b) for a, b in zip(slices, oslices))
+
+
+def test_gpu_side_stream_use_outlives_exit_hooks(dev):
+    """A tensor that carries a record_stream use of a side stream and lives
+    until module teardown (freed after the exit hooks) ends its process
+    cleanly: the side streams are not destroyed before the allocator records
+    its event on them."""
+    code = (
+        "import sys; sys.path.insert(0, sys.argv[1])\n"
+        "import torch, __graft_entry__\n"
+        "ec = __graft_entry__.load_package()\n"
+        "dev = torch.device('cuda:0')\n"
+        "side = ec.side_stream(dev)\n"
+        "held = [torch.randint(0, 256, (1 << 20,), dtype=torch.uint8, device=dev)"
+        " for _ in range(4)]\n"
+        "side.wait_stream(torch.cuda.current_stream(dev))\n"
+        "parity = ec.rs_encode(held, 2, stream=side)\n"
+        "for t in held + list(parity):\n"
+        "    t.record_stream(side)\n"
+        "print('enqueued', flush=True)\n")
+    print("case: side-stream use freed after the exit hooks", flush=True)
+    r = subprocess.run([sys.executable, "-c", code, ROOT], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "enqueued" in r.stdout, (r.returncode, r.stderr[-2000:])
