@@ -28,16 +28,16 @@ def test_header_matches_binding(pkg):
 
 
 def test_integration_stub_binds_every_symbol(pkg):
-    """The ctypes stub a reference maintainer would add (INTEGRATION.md's
-    first code block) names every declared entry point and runs against the
-    built library."""
+    """The ctypes stub a reference maintainer would add (the first Python
+    block of the integration notes at the repository root) names every
+    declared entry point and runs against the built library."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     start = text.index("```python") + len("```python")
     stub = text[start:text.index("```", start)]
     assert sorted(set(re.findall(r"_L\.(ec_\w+)", stub))) == declared_functions()
     stub = stub.replace('ctypes.CDLL("libec_mi355.so")', f'ctypes.CDLL({pkg._lib.LIB_PATH!r})')
     assert pkg._lib.LIB_PATH in stub
-    exec(compile(stub, "INTEGRATION.md stub", "exec"), {})
+    exec(compile(stub, "integration stub", "exec"), {})
 
 
 def test_library_exports_every_declared_symbol(pkg):
