@@ -8,7 +8,10 @@
 // staging thread takes that lock from the training thread only to start
 // and to finish.  Give it an ordinary stream: on MI355X, transfers issued
 // on a CU-masked stream held the host and slowed the training kernels beside
-// them; on ordinary streams they ran asynchronously without doing so.
+// them; on ordinary streams they ran asynchronously without doing so.  (A
+// copy kernel writing the pinned buffer through its device address, on a
+// stream of its own, slowed training's steps more: by up to 2.3x, also on a
+// few CUs.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string.h>
