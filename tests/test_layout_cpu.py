@@ -66,3 +66,18 @@ def test_host_tensors_are_rejected_loudly(pkg):
                  lambda: pkg.encode(cpu, 4, 2, 64)):
         with pytest.raises(ValueError, match="device"):
             call()
+
+
+def test_stripe_descriptors_high_addresses_and_large_tensors(pkg):
+    """Addresses near the top of the 47-bit device range and tensors of tens
+    of GB: the per-unit address arithmetic stays exact (int64 throughout)."""
+    from megatron_lm_amd.layout import stripe_descriptors
+    unit = 4 << 20
+    size = np.array([(24 << 30) + 12345, 0, 7, (3 << 30) + unit], np.int64)
+    base = np.array([0x7F00_0000_0000, 0x7F10_0000_0000, 0x7F20_0000_0000, 0x7FF0_0000_0000],
+                    np.uint64)
+    n_units, P, L = stripe_descriptors(base, size, 8, unit)
+    o2, P2, L2 = loop_layout(base, size, 8, unit)
+    assert n_units == o2.size
+    assert np.array_equal(P, P2) and np.array_equal(L, L2)
+    assert int(P.max()) == 0x7FF0_0000_0000 + (3 << 30)
