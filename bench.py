@@ -53,6 +53,42 @@ def timed(fn, steps: int, warmup: int):
     return wall, start.elapsed_time(end) / steps
 
 
+def settle(fn, seconds: float):
+    """Back-to-back calls of fn() on torch's current stream for at least
+    `seconds` of wall time, in batches that keep the queue full: the GPU's
+    clocks ramp up under sustained load, and a timed region that starts on
+    an idle GPU measures the ramp.  Returns (ms spent, calls made)."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(32):
+            fn()
+        n += 32
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return (time.perf_counter() - t0) * 1e3, n
+
+
+def launch_spread(fn, steps: int):
+    """Per-launch durations (ms) of `steps` back-to-back calls of fn(), from
+    an event pair around each call on torch's current stream: the median
+    and extremes next to the timed region's mean."""
+    import statistics
+    import torch
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return {"median": statistics.median(per), "min": min(per), "max": max(per),
+            "mean": ev[0].elapsed_time(ev[-1]) / steps}
+
+
 def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host, gpu_xor):
     """Repo SIMD CPU encoder (oracle/ec_cpu_fast.c) on a bounded sample: the
     first 64 MiB of each shard, repeated for about `seconds`; all usable
@@ -361,7 +397,7 @@ def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
     the encode is compared with."""
     import ctypes
     import torch
-    path = os.path.join(os.path.dirname(pkg.library_path()), "libec_probe.so")
+    path = os.path.join(ROOT, "probe", "libec_probe.so")
     if not os.path.exists(path):
         return {}
     lib = ctypes.CDLL(path)
@@ -562,7 +598,7 @@ def gf_variants(pkg, synth, dev, seed: int, steps: int) -> int:
     launch and a byte comparison of the parity."""
     import ctypes
     import torch
-    lib = ctypes.CDLL(os.path.join(os.path.dirname(pkg.library_path()), "libec_probe.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "probe", "libec_probe.so"))
     lib.ecp_rs_logexp.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                   ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
     k, m, shard = 6, 3, 256 * MiB
@@ -600,6 +636,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--settle-ms", type=float, default=500.0,
+                    help="back-to-back encodes before the warmup and timed steps, so that "
+                         "the timed region does not measure the GPU's clock ramp")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
@@ -654,16 +693,24 @@ def main() -> int:
     data_bytes = k * shard
     traffic = (k + m) * shard
 
-    log(f"RS(6,3) encode: {args.warmup} warmup + {args.steps} timed steps")
-    wall_ms, ev_ms = timed(lambda: pkg.matvec(coeff, data, out=parity), args.steps, args.warmup)
+    encode = lambda: pkg.matvec(coeff, data, out=parity)
+    settle_ms, settle_n = settle(encode, args.settle_ms * 1e-3)
+    log(f"RS(6,3) encode: settled {settle_ms:.0f} ms ({settle_n} launches), then "
+        f"{args.warmup} warmup + {args.steps} timed steps")
+    wall_ms, ev_ms = timed(encode, args.steps, args.warmup)
     enc_gbs = data_bytes / (wall_ms * 1e-3) / 1e9
     enc_traffic_gbs = traffic / (ev_ms * 1e-3) / 1e9
+    spread = launch_spread(encode, args.steps)
     log(f"encode {enc_gbs:.1f} GB/s data, kernel {ev_ms*1e3:.1f} us, "
-        f"{enc_traffic_gbs:.0f} GB/s HBM traffic")
+        f"{enc_traffic_gbs:.0f} GB/s HBM traffic; per launch median "
+        f"{spread['median']*1e3:.1f} us, min {spread['min']*1e3:.1f}, "
+        f"max {spread['max']*1e3:.1f}")
 
     if args.mode == "headline":
         print(json.dumps({"mode": "headline", "encode_GBps": round(enc_gbs, 2),
                           "kernel_us": round(ev_ms * 1e3, 2),
+                          "kernel_us_median": round(spread["median"] * 1e3, 2),
+                          "settle_ms": round(settle_ms, 1),
                           "traffic_GBps": round(enc_traffic_gbs, 1)}), flush=True)
         return 0
 
@@ -750,7 +797,13 @@ def main() -> int:
                      "traffic": measured_traffic(k, m, shard),
                      "kernel": "rs_kernel<6,3,1>",
                      "algorithmic_bytes_per_launch": traffic,
-                     "kernel_us": round(ev_ms * 1e3, 2)},
+                     "kernel_us": round(ev_ms * 1e3, 2),
+                     "settle_ms": round(settle_ms, 1),
+                     "settle_launches": settle_n,
+                     "launch_us_median": round(spread["median"] * 1e3, 2),
+                     "launch_us_min": round(spread["min"] * 1e3, 2),
+                     "launch_us_max": round(spread["max"] * 1e3, 2),
+                     "launch_us_mean_per_launch_events": round(spread["mean"] * 1e3, 2)},
         "cpu_baseline": cpu,
         "also": {
             "decode_GBps": round(dec_gbs, 2), "decode_lost": lost,

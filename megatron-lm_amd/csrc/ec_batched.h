@@ -1,0 +1,259 @@
+// ec_batched.h — the fixed-size batched stripe kernel (batched_kernel) and
+// its launcher, shared by the plain encode/decode (ec_batched.hip) and the
+// copying encode (ec_batched_copy.hip).
+#pragma once
+
+#include "ec_device.h"
+
+namespace ec {
+namespace {
+
+// ------------------------------------------------ batched stripe kernels --
+// Grid = n_stripes x tiles_per_unit workgroups, stripe-major, so consecutive
+// workgroups stream adjacent bytes of the same k units.  The descriptor of a
+// stripe is uniform across the workgroup (scalar loads).
+
+template <int K, int M>
+struct BatchArgs {
+  const uint64_t* dptr;  // [n_stripes][K]
+  const uint32_t* dlen;  // [n_stripes][K]
+  const uint64_t* pptr;  // [n_stripes][M]
+  const uint32_t* olen;  // [n_stripes][M] valid output bytes, or null = whole units
+  const uint64_t* cptr;  // [n_stripes][K] copy of each data unit, zero-padded to
+                         // unit_bytes (0 = no copy); read only when the kernel copies
+  PermTab tab[M][K];
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;   // tiles of kBlock*U*16 bytes in a unit
+  uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
+  uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
+};
+
+// 16 KiB of zeros in device memory, read-only: on the fast path a unit that
+// ended before the current tile is read from here instead of branching, so
+// the tile's k loads stay unconditional.  (Covers a tile of kBlock * U * 16
+// bytes for U <= 4.)
+__device__ __align__(16) uint8_t g_zero_tile[kBlock * 4 * 16] = {0};
+
+// One tile of a stripe in which no unit ends strictly inside the tile and
+// every output covers it (almost every tile).  src[j] points at the tile's
+// first byte of unit j, or at g_zero_tile if the unit ended before the tile;
+// dst[i] at the tile's first byte of output i.  (A branch around each store
+// for outputs that ended early triples the register count, so such tiles
+// take the edge path instead.)
+//
+// With COPY, cpy[j] points at the tile's first byte of unit j's copy (null:
+// no copy) and the loaded chunk is stored there too: the data is read once
+// for both the parity and the copy.
+template <int K, int M, int U, bool COPY>
+__device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
+                                          uint8_t* const (&cpy)[K],
+                                          const PermTab (&tab)[M][K]) {
+  static_assert(kBlock * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
+  uint4 x[U][K];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t rel = (u * kBlock + threadIdx.x) * 16u;
+#pragma unroll
+    for (int j = 0; j < K; ++j) x[u][j] = load_stream(src[j] + rel);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t rel = (u * kBlock + threadIdx.x) * 16u;
+    uint32_t acc[M][4] = {};
+    gf_matvec16<K, M>(acc, x[u], tab);
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    if constexpr (COPY) {
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (cpy[j]) store_stream(cpy[j] + rel, x[u][j]);
+    }
+  }
+}
+
+// A full tile whose units are not all 16-byte aligned (tensors that are
+// views into a flat buffer at arbitrary offsets): one chunk per lane at a
+// time, each unit read through load_realign (two aligned loads and a byte
+// shift for a misaligned unit); the outputs are aligned.
+template <int K, int M, int U, bool COPY>
+__device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K],
+                                                  uint8_t* const (&dst)[M],
+                                                  uint8_t* const (&cpy)[K],
+                                                  const PermTab (&tab)[M][K]) {
+  constexpr int V = U >= 2 ? 2 : 1;  // chunks per lane in flight together
+#pragma unroll 1
+  for (int u0 = 0; u0 < U; u0 += V) {
+    uint4 x[V][K];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+#pragma unroll
+      for (int j = 0; j < K; ++j) x[v][j] = load_realign(src[j], rel);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+      uint32_t acc[M][4] = {};
+      gf_matvec16<K, M>(acc, x[v], tab);
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      if constexpr (COPY) {
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+          if (cpy[j]) store_stream(cpy[j] + rel, x[v][j]);
+      }
+    }
+  }
+}
+
+// Any other tile (a unit or output ending inside it, an absent unit, a
+// misaligned output): one unit at a time, descriptors re-read from memory,
+// byte-granular at the ends.  Kept as a rolled loop so that its registers
+// stay below the fast path's (the allocator takes the larger of the two).
+//
+// With COPY, each unit's chunk (zeros past its valid length) also goes to
+// its copy, over the whole unit_bytes.
+template <int K, int M, int U, bool COPY>
+__device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, uint32_t base,
+                                          const PermTab (&tab)[M][K]) {
+  for (int u = 0; u < U; ++u) {
+    const uint32_t off = (base + u * kBlock) * 16u;
+    if (off >= a.unit_bytes) continue;
+    uint32_t acc[M][4] = {};
+#pragma unroll 1
+    for (int j = 0; j < K; ++j) {
+      const uint8_t* dj = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
+      uint32_t lj = dj ? a.dlen[(uint64_t)s * K + j] : 0u;
+      lj = lj < a.unit_bytes ? lj : a.unit_bytes;
+      uint4 xj = make_uint4(0u, 0u, 0u, 0u);
+      if (off < lj) {
+        xj = load_unit(dj, off, lj);
+        Fields f[4];
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(xj, dd));
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+          const PermTab t = tab[i][j];
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+        }
+      }
+      if constexpr (COPY) {
+        uint8_t* cj = reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]);
+        if (cj) store_unit(cj, off, xj);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      uint8_t* pi = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+      uint32_t li = a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes;
+      li = pi ? (li < a.unit_bytes ? li : a.unit_bytes) : 0u;
+      if (off < li)
+        store_unit_len(pi, off, li, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  }
+}
+
+template <int K, int M, int U, bool COPY>
+__global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  // Workgroup b covers tiles [t0, t1) of one stripe: the descriptor loads and
+  // table staging are paid once per span, not once per 4-8 KiB tile.
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  // Stripe-uniform facts (scalar registers): addresses, valid lengths, and
+  // whether everything is 16-byte aligned.
+  const uint8_t* d[K];
+  uint32_t len[K];
+  bool in_aligned = true, out_aligned = true;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
+    const uint32_t l = d[j] ? a.dlen[(uint64_t)s * K + j] : 0u;
+    len[j] = l < a.unit_bytes ? l : a.unit_bytes;
+    in_aligned &= (reinterpret_cast<uintptr_t>(d[j]) & 15u) == 0;
+  }
+  uint8_t* p[M];
+  uint32_t olen[M];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    const uint32_t l = p[i] ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
+    olen[i] = l < a.unit_bytes ? l : a.unit_bytes;
+    out_aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+  }
+  uint8_t* c[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    c[j] = COPY ? reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]) : nullptr;
+    out_aligned &= (reinterpret_cast<uintptr_t>(c[j]) & 15u) == 0;
+  }
+  constexpr uint32_t kTileBytes = kBlock * U * 16u;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t base = t * (kBlock * U) + threadIdx.x;
+    const uint32_t lo = t * kTileBytes, hi = lo + kTileBytes;
+    // A tile is an edge tile when some unit ends strictly inside it or some
+    // output does not cover it.
+    const uint8_t* src[K];
+    uint8_t* dst[M];
+    uint8_t* cpy[K];
+    bool edge = !out_aligned;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      src[j] = len[j] >= hi ? d[j] + lo : g_zero_tile;
+      edge |= len[j] > lo && len[j] < hi;
+      cpy[j] = c[j] ? c[j] + lo : nullptr;
+      if (COPY) edge |= c[j] && a.unit_bytes < hi;  // a copy always spans the unit
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      dst[i] = p[i] + lo;
+      edge |= olen[i] < hi;
+    }
+    if (edge)
+      tile_edge<K, M, U, COPY>(a, s, base, tab);
+    else if (in_aligned)
+      tile_full<K, M, U, COPY>(src, dst, cpy, tab);
+    else
+      tile_full_realign<K, M, U, COPY>(src, dst, cpy, tab);
+  }
+}
+
+template <int K, int M, int U, bool COPY>
+int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
+                     const uint64_t* pptr, const uint32_t* olen, const uint64_t* cptr,
+                     uint32_t n_stripes, uint32_t unit_bytes, hipStream_t st) {
+  BatchArgs<K, M> a;
+  a.dptr = dptr;
+  a.dlen = dlen;
+  a.pptr = pptr;
+  a.olen = olen;
+  a.cptr = cptr;
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  const uint32_t unit16 = unit_bytes / 16u;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
+  // A workgroup walks up to span_bytes() of each unit (at least one tile),
+  // keeping at least 2048 workgroups (8 per CU) in the launch.
+  const uint32_t tile_bytes = kBlock * U * 16u;
+  uint64_t tpb = span_bytes(unit_bytes) / tile_bytes;
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  hipLaunchKernelGGL((batched_kernel<K, M, U, COPY>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                     st, a);
+  return hip_status();
+}
+
+}  // namespace
+}  // namespace ec

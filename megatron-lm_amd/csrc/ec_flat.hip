@@ -1,0 +1,443 @@
+// ec_flat.hip — the flat-shard kernels and entry points of the C ABI:
+// ec_xor_encode, ec_rs_encode, ec_rs_decode (k equal-size shards in, m out),
+// and ec_stream_create / ec_stream_destroy.  Helpers, the GF multiply and
+// the streaming accesses are in ec_device.h.
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <array>
+#include <utility>
+#include <vector>
+
+#include "ec_device.h"
+
+namespace ec {
+namespace {
+
+// ------------------------------------------------ fast matrix-vector kernel --
+// parity_i = XOR_j C[i][j] * data_j over n16 16-byte chunks; all pointers
+// 16-byte aligned.  Encode and decode both run this kernel (decode with the
+// host-inverted rows over the survivors).
+
+template <int K, int M>
+struct RsArgs {
+  const uint8_t* data[K];
+  uint8_t* out[M];
+  PermTab tab[M][K];
+  uint64_t n16;
+};
+
+template <int K, int M, int U>
+__global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  const uint64_t tile = (uint64_t)kBlock * U;
+  const uint64_t stride = (uint64_t)gridDim.x * tile;
+  for (uint64_t base = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * tile + threadIdx.x;
+       base < a.n16; base += stride) {
+    uint4 x[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+      if (idx < a.n16) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
+      } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kBlock;
+      uint32_t acc[M][4] = {};
+      gf_matvec16<K, M>(acc, x[u], tab);
+      if (idx < a.n16) {
+#pragma unroll
+        for (int i = 0; i < M; ++i)
+          store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- XOR kernel --
+
+template <int K>
+struct XorArgs {
+  const uint8_t* data[K];
+  uint8_t* out;
+  uint64_t n16;
+};
+
+__device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uint4& c) {
+  return make_uint4(xor3(a.x, b.x, c.x), xor3(a.y, b.y, c.y), xor3(a.z, b.z, c.z),
+                    xor3(a.w, b.w, c.w));
+}
+
+// XOR parity: 512-lane workgroups in launch order (measured on MI355X for
+// XOR(4) over 64 MiB shards: 6.37 TB/s of HBM traffic; 6.21 with 256 lanes;
+// 5.68 with one tile window per XCD and 6.00 with split_tile's two, which
+// only pay off for the RS kernel).
+constexpr int kXorBlock = 512;
+
+template <int K, int U>
+__global__ void __launch_bounds__(kXorBlock) xor_kernel(const XorArgs<K> a) {
+  const uint64_t tile = (uint64_t)kXorBlock * U;
+  const uint64_t stride = (uint64_t)gridDim.x * tile;
+  for (uint64_t base = (uint64_t)blockIdx.x * tile + threadIdx.x; base < a.n16;
+       base += stride) {
+    uint4 x[U][K];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kXorBlock;
+      if (idx < a.n16) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
+      } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + (uint64_t)u * kXorBlock;
+      uint4 acc = x[u][0];
+      int j = 1;
+#pragma unroll
+      for (; j + 1 < K; j += 2) acc = xor3v(acc, x[u][j], x[u][j + 1]);
+      if (j < K)
+        acc = make_uint4(acc.x ^ x[u][j].x, acc.y ^ x[u][j].y, acc.z ^ x[u][j].z,
+                         acc.w ^ x[u][j].w);
+      if (idx < a.n16) {
+        if (K == 1)  // a plain copy: streaming stores measured 3 % faster
+          store_stream(a.out + idx * 16, acc);
+        else
+          reinterpret_cast<uint4*>(a.out)[idx] = acc;
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------- generic kernel --
+// Any k <= EC_MAX_K, m <= EC_MAX_M and any alignment: byte loads and stores,
+// four bytes per lane, permute tables built in LDS by the workgroup.  Used for
+// shard counts beyond the instantiated ones, misaligned pointers and the
+// sub-16-byte tail of the fast kernels.
+
+struct GenArgs {
+  const uint8_t* data[EC_MAX_K];
+  uint8_t* out[EC_MAX_M];
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];
+  uint64_t n;
+  int k, m;
+};
+
+__global__ void __launch_bounds__(kBlock) generic_kernel(const GenArgs a) {
+  __shared__ PermTab tab[EC_MAX_M * EC_MAX_K];
+  for (int t = threadIdx.x; t < a.m * a.k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
+  __syncthreads();
+  const uint64_t n4 = (a.n + 3) / 4;
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t q = (uint64_t)blockIdx.x * kBlock + threadIdx.x; q < n4; q += stride) {
+    const uint64_t b0 = q * 4;
+    const int nb = (int)((a.n - b0) < 4 ? (a.n - b0) : 4);
+    uint32_t acc[EC_MAX_M];
+    for (int i = 0; i < a.m; ++i) acc[i] = 0;
+    for (int j = 0; j < a.k; ++j) {
+      uint32_t w = 0;
+      for (int b = 0; b < nb; ++b) w |= (uint32_t)a.data[j][b0 + b] << (8 * b);
+      const Fields f = fields(w);
+      for (int i = 0; i < a.m; ++i) acc[i] = mac1(acc[i], tab[i * a.k + j], f);
+    }
+    for (int i = 0; i < a.m; ++i)
+      for (int b = 0; b < nb; ++b) a.out[i][b0 + b] = (uint8_t)(acc[i] >> (8 * b));
+  }
+}
+
+// ------------------------------------------------------------ wide kernel --
+// Codes past the instantiated fast path: see kWideGroup in ec_device.h.
+struct WideArgs {
+  const uint8_t* data[EC_MAX_K];
+  uint8_t* out[EC_MAX_M];
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];  // row-major m x k
+  uint64_t n16;
+  int k;
+};
+
+template <int M>
+__global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
+  __shared__ PermTab tab[M * EC_MAX_K];
+  const int k = a.k;
+  for (int t = threadIdx.x; t < M * k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
+  __syncthreads();
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t idx = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * kBlock + threadIdx.x;
+       idx < a.n16; idx += stride) {
+    uint32_t acc[M][4] = {};
+    for (int j0 = 0; j0 < k; j0 += kWideGroup) {
+      uint4 x[kWideGroup];
+#pragma unroll
+      for (int g = 0; g < kWideGroup; ++g)
+        x[g] = j0 + g < k ? load_realign(a.data[j0 + g], idx * 16) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int g = 0; g < kWideGroup; g += kWidePair<M>()) {
+        if (j0 + g >= k) break;
+        if constexpr (kWidePair<M>() == 2) {
+          // Two coefficients per step (three XOR3 instead of two XOR3 and
+          // two XOR).  x[g + 1] is zero past k and a zero byte's products
+          // are zero, so the pair form is exact for an odd k as well.
+          Fields fa[4], fb[4];
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) {
+            fa[dd] = fields(word(x[g], dd));
+            fb[dd] = fields(word(x[g + 1], dd));
+          }
+          const int jb = j0 + g + 1 < k ? j0 + g + 1 : j0 + g;
+#pragma unroll
+          for (int i = 0; i < M; ++i) {
+            // Read each table right before its uses (see gf_matvec16).
+            asm volatile("" ::: "memory");
+            const PermTab ta = tab[i * k + j0 + g], tb = tab[i * k + jb];
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac2(acc[i][dd], ta, fa[dd], tb, fb[dd]);
+          }
+        } else {
+          Fields f[4];
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x[g], dd));
+#pragma unroll
+          for (int i = 0; i < M; ++i) {
+            asm volatile("" ::: "memory");
+            const PermTab t = tab[i * k + j0 + g];
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+  }
+}
+
+// ---------------------------------------------------------- host launch --
+
+template <int K, int M>
+int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, uint64_t n16,
+              hipStream_t st) {
+  RsArgs<K, M> a;
+  for (int j = 0; j < K; ++j) a.data[j] = d[j];
+  for (int i = 0; i < M; ++i) a.out[i] = o[i];
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  a.n16 = n16;
+  // One 16-byte chunk per lane per shard: with the two-window order this beat
+  // two chunks by 2-6 % for k <= 8 (k > 8 needs U = 1 for registers anyway).
+  constexpr int U = 1;
+  hipLaunchKernelGGL((rs_kernel<K, M, U>), dim3(grid_for(n16, U)), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+template <int M>
+int launch_wide(const uint8_t* coeff, int k, const uint8_t* const* d, uint8_t* const* o,
+                uint64_t n16, hipStream_t st) {
+  WideArgs a;
+  for (int j = 0; j < k; ++j) a.data[j] = d[j];
+  for (int i = 0; i < M; ++i) a.out[i] = o[i];
+  for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
+  a.n16 = n16;
+  a.k = k;
+  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid_for(n16, 1)), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+template <int K>
+int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st) {
+  XorArgs<K> a;
+  for (int j = 0; j < K; ++j) a.data[j] = d[j];
+  a.out = o;
+  a.n16 = n16;
+  constexpr int U = unroll_for<K>();
+  hipLaunchKernelGGL((xor_kernel<K, U>), dim3(grid_for(n16, U * (kXorBlock / kBlock))),
+                     dim3(kXorBlock), 0, st, a);
+  return hip_status();
+}
+
+using RsFn = int (*)(const uint8_t*, const uint8_t* const*, uint8_t* const*, uint64_t,
+                     hipStream_t);
+using XorFn = int (*)(const uint8_t* const*, uint8_t*, uint64_t, hipStream_t);
+
+template <int K, int... Ms>
+constexpr auto rs_row(std::integer_sequence<int, Ms...>) {
+  return std::array<RsFn, sizeof...(Ms)>{&launch_rs<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto rs_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<RsFn, kFastMaxM>, sizeof...(Ks)>{
+      rs_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
+template <int... Ks>
+constexpr auto xor_table(std::integer_sequence<int, Ks...>) {
+  return std::array<XorFn, sizeof...(Ks)>{&launch_xor<Ks + 1>...};
+}
+using WideFn = int (*)(const uint8_t*, int, const uint8_t* const*, uint8_t* const*, uint64_t,
+                       hipStream_t);
+template <int... Ms>
+constexpr auto wide_table(std::integer_sequence<int, Ms...>) {
+  return std::array<WideFn, sizeof...(Ms)>{&launch_wide<Ms + 1>...};
+}
+
+const auto kRsTable = rs_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kXorTable = xor_table(std::make_integer_sequence<int, kFastMaxK>{});
+const auto kWideTable = wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
+
+int launch_generic(const uint8_t* coeff, int k, int m, const uint8_t* const* d,
+                   uint8_t* const* o, uint64_t offset, uint64_t n, hipStream_t st) {
+  GenArgs a;
+  for (int j = 0; j < k; ++j) a.data[j] = d[j] + offset;
+  for (int i = 0; i < m; ++i) a.out[i] = o[i] + offset;
+  for (int t = 0; t < m * k; ++t) a.coeff[t] = coeff[t];
+  a.n = n;
+  a.k = k;
+  a.m = m;
+  const uint64_t n4 = (n + 3) / 4;
+  uint64_t blocks = (n4 + kBlock - 1) / kBlock;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(generic_kernel, dim3((unsigned)(blocks ? blocks : 1)), dim3(kBlock), 0, st,
+                     a);
+  return hip_status();
+}
+
+// Common misalignment of a set of addresses modulo 16, or -1 if they differ.
+inline int common_skew(const uint8_t* const* a, int n, int skew) {
+  for (int i = 0; i < n; ++i) {
+    const int s = (int)(reinterpret_cast<uintptr_t>(a[i]) & 15u);
+    if (skew < 0) skew = s;
+    else if (s != skew) return -1;
+  }
+  return skew;
+}
+
+int matvec(const uint8_t* coeff, int k, int m, const uint8_t* const* d, uint8_t* const* o,
+           uint64_t nbytes, hipStream_t st) {
+  if (!coeff || !d || !o) return EC_EINVAL;
+  if (k < 1 || m < 1) return EC_EINVAL;
+  if (k > EC_MAX_K || m > EC_MAX_M) return EC_ERANGE;
+  if (nbytes == 0) return EC_OK;  // empty shards may have null addresses
+  for (int j = 0; j < k; ++j)
+    if (!d[j]) return EC_EINVAL;
+  for (int i = 0; i < m; ++i)
+    if (!o[i]) return EC_EINVAL;
+  // The outputs fix the frame: the bytes up to their next 16-byte boundary
+  // run through the byte kernel, the 16-byte columns after it through a
+  // vector kernel (the fast one when every input shares the outputs'
+  // misalignment, else the wide one, which realigns each input), and the
+  // last partial column through the byte kernel.  Outputs of different
+  // misalignments take the byte kernel throughout.
+  const int skew = common_skew(o, m, -1);
+  if (skew < 0) return launch_generic(coeff, k, m, d, o, 0, nbytes, st);
+  const bool same = common_skew(d, k, skew) == skew;
+  uint64_t head = skew ? 16u - (uint64_t)skew : 0;
+  if (head > nbytes) head = nbytes;
+  int s = EC_OK;
+  if (head) s = launch_generic(coeff, k, m, d, o, 0, head, st);
+  const uint64_t n16 = (nbytes - head) / 16;
+  if (s == EC_OK && n16) {
+    const uint8_t* da[EC_MAX_K];
+    uint8_t* oa[EC_MAX_M];
+    for (int j = 0; j < k; ++j) da[j] = d[j] + head;
+    for (int i = 0; i < m; ++i) oa[i] = o[i] + head;
+    if (same && k <= kFastMaxK && m <= kFastMaxM)
+      s = kRsTable[k - 1][m - 1](coeff, da, oa, n16, st);
+    else
+      s = kWideTable[m - 1](coeff, k, da, oa, n16, st);
+  }
+  const uint64_t done = head + n16 * 16;
+  if (s == EC_OK && done < nbytes) s = launch_generic(coeff, k, m, d, o, done, nbytes - done, st);
+  return s;
+}
+
+}  // namespace
+}  // namespace ec
+
+extern "C" {
+
+int ec_xor_encode(const uint8_t* const* d_data, int k, uint8_t* d_parity, uint64_t nbytes,
+                  ec_stream_t stream) {
+  if (!d_data || k < 1) return EC_EINVAL;
+  if (k > EC_MAX_K) return EC_ERANGE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (nbytes == 0) return EC_OK;  // empty shards may have null addresses
+  if (!d_parity) return EC_EINVAL;
+  for (int j = 0; j < k; ++j)
+    if (!d_data[j]) return EC_EINVAL;
+  uint8_t ones[EC_MAX_K];
+  for (int j = 0; j < k; ++j) ones[j] = 1;  // 1*x = x: XOR parity via the generic path
+  uint8_t* const out[1] = {d_parity};
+  const int skew = ec::common_skew(out, 1, -1);
+  const bool same = ec::common_skew(d_data, k, skew) == skew;
+  uint64_t head = skew ? 16u - (uint64_t)skew : 0;
+  if (head > nbytes) head = nbytes;
+  int s = EC_OK;
+  if (head) s = ec::launch_generic(ones, k, 1, d_data, out, 0, head, st);
+  const uint64_t n16 = (nbytes - head) / 16;
+  if (s == EC_OK && n16) {
+    const uint8_t* da[EC_MAX_K];
+    for (int j = 0; j < k; ++j) da[j] = d_data[j] + head;
+    uint8_t* const oa[1] = {d_parity + head};
+    s = same && k <= ec::kFastMaxK ? ec::kXorTable[k - 1](da, d_parity + head, n16, st)
+                                   : ec::kWideTable[0](ones, k, da, oa, n16, st);
+  }
+  const uint64_t done = head + n16 * 16;
+  if (s == EC_OK && done < nbytes)
+    s = ec::launch_generic(ones, k, 1, d_data, out, done, nbytes - done, st);
+  return s;
+}
+
+int ec_rs_encode(const uint8_t* coeff, int k, int m, const uint8_t* const* d_data,
+                 uint8_t* const* d_parity, uint64_t nbytes, ec_stream_t stream) {
+  return ec::matvec(coeff, k, m, d_data, d_parity, nbytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_rs_decode(const uint8_t* rows, int k, int e, const uint8_t* const* d_survivors,
+                 uint8_t* const* d_out, uint64_t nbytes, ec_stream_t stream) {
+  return ec::matvec(rows, k, e, d_survivors, d_out, nbytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int ec_stream_create(int device, int n_cus, ec_stream_t* out) {
+  if (!out) return EC_EINVAL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return EC_EHIP;
+  if (device < 0 || device >= count) return EC_EINVAL;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    return EC_EHIP;
+  const int n = (n_cus <= 0 || n_cus > cus) ? cus : n_cus;
+  std::vector<uint32_t> mask((cus + 31) / 32, 0u);
+  for (int c = 0; c < n; ++c) mask[c / 32] |= 1u << (c % 32);
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
+  if (prev != device && hipSetDevice(device) != hipSuccess) return EC_EHIP;
+  hipStream_t st = nullptr;
+  const hipError_t e =
+      hipExtStreamCreateWithCUMask(&st, static_cast<uint32_t>(mask.size()), mask.data());
+  if (prev != device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return EC_EHIP;
+  }
+  *out = st;
+  return EC_OK;
+}
+
+int ec_stream_destroy(ec_stream_t stream) {
+  if (!stream) return EC_EINVAL;
+  return hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)) == hipSuccess ? EC_OK : EC_EHIP;
+}
+
+}  // extern "C"

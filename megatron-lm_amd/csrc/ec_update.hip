@@ -1,0 +1,403 @@
+// ec_update.hip — ec_parity_update (update_kernel, k <= 16, m <= 4) and the
+// batched kernels for wide codes (batched_wide_kernel, update_wide_kernel:
+// k at run time, up to EC_MAX_K x EC_MAX_M), which ec_batched.hip and
+// ec_batched_copy.hip reach through batched_wide().
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <array>
+#include <utility>
+
+#include "ec_device.h"
+
+namespace ec {
+namespace {
+
+template <int K, int M>
+struct UpdateArgs {
+  const uint64_t* nptr;  // [n_stripes][K], 0 = unit unchanged
+  const uint64_t* optr;  // [n_stripes][K]
+  const uint32_t* len;   // [n_stripes][K]
+  const uint64_t* pptr;  // [n_stripes][M]
+  PermTab tab[M][K];
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;   // tiles of kBlock*16 bytes in a unit
+  uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
+  uint32_t blocks_per_unit;
+};
+
+// Incremental update: each workgroup walks a span of tiles of one changed
+// stripe.  The stripe's descriptors (which units changed, where their old
+// and new bytes are, their lengths) are read once per span into scalar
+// registers; a tile inside every changed unit, with everything 16-byte
+// aligned, takes plain vector loads, any other tile the byte-granular path.
+template <int K, int M>
+__global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a) {
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  const uint8_t* nw[K];
+  const uint8_t* od[K];
+  uint32_t len[K];
+  uint32_t full = a.unit_bytes;
+  bool aligned = true, in_aligned = true;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    nw[j] = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
+    od[j] = nw[j] ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]) : nullptr;
+    const uint32_t l = nw[j] ? a.len[(uint64_t)s * K + j] : 0u;
+    len[j] = l < a.unit_bytes ? l : a.unit_bytes;
+    if (nw[j]) {
+      full = len[j] < full ? len[j] : full;
+      in_aligned &=
+          ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
+    }
+  }
+  // Misaligned units (views at arbitrary offsets) are realigned on the fast
+  // path (load_realign); only the parity must be 16-byte aligned for it.  The
+  // aligned case keeps plain loads: realigning every load cost the 1 %
+  // update 5 % (0.338 -> 0.356 ms).
+  uint8_t* p[M];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+  }
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t off = (t * kBlock + threadIdx.x) * 16u;
+    if (off >= a.unit_bytes) continue;
+    const bool fast = aligned && (t + 1) * (kBlock * 16u) <= full;
+    uint32_t acc[M][4] = {};
+    // The parity loads do not depend on the delta: issue them first so that
+    // they are in flight together with the unit loads.
+    uint4 pv[M];
+    if (fast) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) pv[i] = load_stream(p[i] + off);
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      if (nw[j] == nullptr) continue;  // uniform: unchanged unit
+      if (!fast && off >= len[j]) continue;
+      uint4 vn, vo;
+      if (fast && in_aligned) {
+        vn = load_stream(nw[j] + off);
+        vo = load_stream(od[j] + off);
+      } else if (fast) {
+        vn = load_realign(nw[j], off);
+        vo = load_realign(od[j], off);
+      } else {
+        vn = load_unit(nw[j], off, len[j]);
+        vo = load_unit(od[j], off, len[j]);
+      }
+      const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
+      Fields f[4];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(dl, dd));
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        asm volatile("" ::: "memory");
+        const PermTab tj = tab[i][j];
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], tj, f[dd]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      const uint4 v = fast ? pv[i] : load_unit(p[i], off, a.unit_bytes);
+      const uint4 w = make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]);
+      if (fast)
+        store_stream(p[i] + off, w);
+      else
+        store_unit(p[i], off, w);
+    }
+  }
+}
+
+// --------------------------------------- batched kernels for wide codes --
+// The batched encode/decode and the parity update for codes past the
+// instantiated fast path (k > 16 or m > 4): k at run time, M a template
+// parameter, one 16-byte chunk per lane (4 KiB tiles).  A workgroup stages
+// its stripe's descriptors and the m x k tables in LDS; fast tiles issue the
+// unit loads in groups of kWideGroup, edge tiles take the units one at a
+// time with byte-granular ends, as in the fixed-size kernels.
+constexpr uint32_t kWideTile = kBlock * 16u;
+
+struct BatchWideArgs {
+  const uint64_t* dptr;  // [n_stripes][k] (update: new units, 0 = unchanged)
+  const uint32_t* dlen;  // [n_stripes][k]
+  const uint64_t* optr;  // update: [n_stripes][k] old units; otherwise unused
+  const uint64_t* pptr;  // [n_stripes][m]
+  const uint32_t* olen;  // [n_stripes][m] valid output bytes, or null = whole units
+  uint8_t coeff[EC_MAX_M * EC_MAX_K];  // row-major m x k
+  uint32_t unit_bytes;
+  uint32_t tiles_per_unit;
+  uint32_t tiles_per_block;
+  uint32_t blocks_per_unit;
+  int k;
+};
+
+template <int M>
+struct WideStripe {
+  PermTab tab[M * EC_MAX_K];
+  const uint8_t* d[EC_MAX_K];
+  const uint8_t* o[EC_MAX_K];
+  uint32_t len[EC_MAX_K];
+  uint8_t* p[M];
+  uint32_t plen[M];
+};
+
+// Tables and stripe s's descriptors into LDS.  Returns, after a barrier,
+// whether any unit or output address is not 16-byte aligned (uniform).
+template <int M>
+__device__ __forceinline__ bool stage_wide(WideStripe<M>& w, const BatchWideArgs& a, uint32_t s,
+                                           bool update) {
+  const int k = a.k;
+  const uint32_t t = threadIdx.x;
+  for (uint32_t i = t; i < (uint32_t)(M * k); i += kBlock) w.tab[i] = dev_perm_tab(a.coeff[i]);
+  if (t < (uint32_t)k) {
+    const uint8_t* d = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * k + t]);
+    const uint32_t l = d ? a.dlen[(uint64_t)s * k + t] : 0u;
+    const uint8_t* o = update && d ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * k + t])
+                                   : nullptr;
+    w.d[t] = d;
+    w.o[t] = o;
+    w.len[t] = l < a.unit_bytes ? l : a.unit_bytes;
+  } else if (t >= 64 && t < 64 + M) {
+    const uint32_t i = t - 64;
+    uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
+    const uint32_t l = p ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
+    w.p[i] = p;
+    w.plen[i] = l < a.unit_bytes ? l : a.unit_bytes;
+  }
+  __syncthreads();
+  uintptr_t bits = 0;
+  for (int j = 0; j < k; ++j)
+    bits |= reinterpret_cast<uintptr_t>(w.d[j]) | reinterpret_cast<uintptr_t>(w.o[j]);
+#pragma unroll
+  for (int i = 0; i < M; ++i) bits |= reinterpret_cast<uintptr_t>(w.p[i]);
+  return (bits & 15u) != 0;
+}
+
+template <int M>
+__device__ __forceinline__ void wide_mac(uint32_t (&acc)[M][4], const uint4& x,
+                                         const PermTab* col, int k) {
+  Fields f[4];
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(x, dd));
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    asm volatile("" ::: "memory");
+    const PermTab t = col[i * k];
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], t, f[dd]);
+  }
+}
+
+template <int M>
+__global__ void __launch_bounds__(kBlock) batched_wide_kernel(const BatchWideArgs a) {
+  __shared__ WideStripe<M> w;
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  const bool misaligned = stage_wide<M>(w, a, s, false);
+  const int k = a.k;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t lo = t * kWideTile, hi = lo + kWideTile;
+    const uint32_t off = lo + threadIdx.x * 16u;
+    bool edge = misaligned;
+    for (int j = 0; j < k; ++j) edge |= w.len[j] > lo && w.len[j] < hi;
+#pragma unroll
+    for (int i = 0; i < M; ++i) edge |= w.plen[i] < hi;
+    uint32_t acc[M][4] = {};
+    if (!edge) {
+      for (int j0 = 0; j0 < k; j0 += kWideGroup) {
+        uint4 x[kWideGroup];
+#pragma unroll
+        for (int g = 0; g < kWideGroup; ++g) {
+          const int j = j0 + g;
+          x[g] = j < k && w.len[j] >= hi ? load_stream(w.d[j] + off) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < kWideGroup; ++g) {
+          if (j0 + g >= k) break;
+          wide_mac<M>(acc, x[g], &w.tab[j0 + g], k);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        store_stream(w.p[i] + off, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    } else {
+      if (off >= a.unit_bytes) continue;
+#pragma unroll 1
+      for (int j = 0; j < k; ++j) {
+        if (off >= w.len[j]) continue;
+        wide_mac<M>(acc, load_unit(w.d[j], off, w.len[j]), &w.tab[j], k);
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+        if (off < w.plen[i])
+          store_unit_len(w.p[i], off, w.plen[i],
+                         make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  }
+}
+
+// parity[s][i] ^= C[i][j] * (new[s][j] ^ old[s][j]) for the changed units.
+template <int M>
+__global__ void __launch_bounds__(kBlock) update_wide_kernel(const BatchWideArgs a) {
+  __shared__ WideStripe<M> w;
+  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
+  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  stage_wide<M>(w, a, s, true);
+  const int k = a.k;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t off = t * kWideTile + threadIdx.x * 16u;
+    if (off >= a.unit_bytes) continue;
+    uint32_t acc[M][4] = {};
+    uint4 pv[M];  // the parity does not depend on the delta: load it first
+#pragma unroll
+    for (int i = 0; i < M; ++i) pv[i] = load_unit(w.p[i], off, a.unit_bytes);
+#pragma unroll 1
+    for (int j = 0; j < k; ++j) {
+      if (w.d[j] == nullptr || off >= w.len[j]) continue;  // unchanged unit, or past its end
+      const uint4 vn = load_unit(w.d[j], off, w.len[j]);
+      const uint4 vo = load_unit(w.o[j], off, w.len[j]);
+      wide_mac<M>(acc, make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w),
+                  &w.tab[j], k);
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+      store_unit(w.p[i], off, make_uint4(pv[i].x ^ acc[i][0], pv[i].y ^ acc[i][1],
+                                         pv[i].z ^ acc[i][2], pv[i].w ^ acc[i][3]));
+  }
+}
+
+template <int K, int M>
+int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* optr,
+                  const uint32_t* len, const uint64_t* pptr, uint32_t n_stripes,
+                  uint32_t unit_bytes, hipStream_t st) {
+  UpdateArgs<K, M> a;
+  a.nptr = nptr;
+  a.optr = optr;
+  a.len = len;
+  a.pptr = pptr;
+  for (int i = 0; i < M; ++i)
+    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
+  const uint32_t unit16 = unit_bytes / 16u;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit16 + kBlock - 1) / kBlock;
+  // One tile per workgroup: each tile is a dependent chain (unit and parity
+  // loads, then the parity store), so the update wants as many workgroups
+  // in flight as it has tiles.  Measured for the 1 % update of 3,000 ragged
+  // tensors in 64 KiB units (RS(12,4), 2,993 stripes): 3-tile spans 0.382 ms,
+  // one tile 0.343 ms, one tile with the parity loads issued first 0.338 ms.
+  // Spans grow only to keep the grid near 2^30 workgroups.
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  uint64_t tpb = (total_tiles + 0x3fffffffull) >> 30;
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  hipLaunchKernelGGL((update_kernel<K, M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+// Wide codes through the batched kernels: encode / decode (update = false,
+// optr unused) or the parity update.  The same span rules as the fixed-size
+// launchers: spans of span_bytes() with at least 2048 workgroups for the
+// encode, one tile per workgroup for the update.
+template <int M>
+int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
+                        const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
+                        uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st) {
+  BatchWideArgs a;
+  a.dptr = dptr;
+  a.dlen = dlen;
+  a.optr = optr;
+  a.pptr = pptr;
+  a.olen = olen;
+  for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
+  a.k = k;
+  a.unit_bytes = unit_bytes;
+  a.tiles_per_unit = (unit_bytes / 16u + kBlock - 1) / kBlock;
+  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
+  uint64_t tpb = 1;
+  if (!update) {
+    tpb = span_bytes(unit_bytes) / kWideTile;
+    if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
+  } else {
+    tpb = (total_tiles + 0x3fffffffull) >> 30;
+  }
+  if (tpb < 1) tpb = 1;
+  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
+  a.tiles_per_block = (uint32_t)tpb;
+  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
+  if (blocks > 0x7fffffffull) return EC_ERANGE;
+  if (update)
+    hipLaunchKernelGGL((update_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((batched_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  return hip_status();
+}
+
+using UpdFn = int (*)(const uint8_t*, const uint64_t*, const uint64_t*, const uint32_t*,
+                      const uint64_t*, uint32_t, uint32_t, hipStream_t);
+
+template <int K, int... Ms>
+constexpr auto upd_row(std::integer_sequence<int, Ms...>) {
+  return std::array<UpdFn, sizeof...(Ms)>{&launch_update<K, Ms + 1>...};
+}
+template <int... Ks>
+constexpr auto upd_table(std::integer_sequence<int, Ks...>) {
+  return std::array<std::array<UpdFn, kFastMaxM>, sizeof...(Ks)>{
+      upd_row<Ks + 1>(std::make_integer_sequence<int, kFastMaxM>{})...};
+}
+const auto kUpdTable = upd_table(std::make_integer_sequence<int, kFastMaxK>{});
+using BatchWideFn = int (*)(const uint8_t*, int, const uint64_t*, const uint32_t*,
+                            const uint64_t*, const uint64_t*, const uint32_t*, uint32_t, uint32_t,
+                            bool, hipStream_t);
+template <int... Ms>
+constexpr auto batch_wide_table(std::integer_sequence<int, Ms...>) {
+  return std::array<BatchWideFn, sizeof...(Ms)>{&launch_batched_wide<Ms + 1>...};
+}
+const auto kBatchWideTable = batch_wide_table(std::make_integer_sequence<int, EC_MAX_M>{});
+
+
+}  // namespace
+
+int batched_wide(int m, const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
+                 const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
+                 uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st) {
+  if (m < 1 || m > EC_MAX_M || k < 1 || k > EC_MAX_K) return EC_ERANGE;
+  return kBatchWideTable[m - 1](coeff, k, dptr, dlen, optr, pptr, olen, n_stripes, unit_bytes,
+                                update, st);
+}
+
+}  // namespace ec
+
+extern "C" {
+
+int ec_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* d_new_ptrs,
+                     const uint64_t* d_old_ptrs, const uint32_t* d_len,
+                     const uint64_t* d_parity_ptrs, uint32_t n_stripes, uint32_t unit_bytes,
+                     ec_stream_t stream) {
+  int s = ec::check_batch(coeff, k, m, d_new_ptrs, d_old_ptrs, d_parity_ptrs, unit_bytes);
+  if (s != EC_OK) return s;
+  if (!d_len) return EC_EINVAL;
+  if (n_stripes == 0) return EC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!ec::fast_shape(k, m))
+    return ec::kBatchWideTable[m - 1](coeff, k, d_new_ptrs, d_len, d_old_ptrs, d_parity_ptrs,
+                                      nullptr, n_stripes, unit_bytes, true, st);
+  return ec::kUpdTable[k - 1][m - 1](coeff, d_new_ptrs, d_old_ptrs, d_len, d_parity_ptrs,
+                                     n_stripes, unit_bytes, st);
+}
+
+}  // extern "C"

@@ -10,10 +10,12 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 
 @pytest.fixture(scope="module")
 def probe(pkg):
-    path = os.path.join(os.path.dirname(pkg.library_path()), "libec_probe.so")
+    path = os.path.join(ROOT, "probe", "libec_probe.so")
     lib = ctypes.CDLL(path)
     lib.ecp_stream.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
