@@ -89,64 +89,150 @@ def launch_spread(fn, steps: int):
             "mean": ev[0].elapsed_time(ev[-1]) / steps}
 
 
-def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host, gpu_xor):
-    """Repo SIMD CPU encoder (oracle/ec_cpu_fast.c) on a bounded sample: the
-    first 64 MiB of each shard, repeated for about `seconds`; all usable
-    cores (at most 16, the box's share per GPU) and one core.  Also the gate
-    that GPU and CPU agree byte for byte on that sample (RS parity) and on the
-    whole XOR config."""
+def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host, gpu_xor,
+                 lost, batched_cpu) -> dict:
+    """The repo's multithreaded SIMD CPU encoder (oracle/ec_cpu_fast.c; the
+    reference ships none) on bounded samples of the same bytes the GPU coded,
+    all usable cores (at most 16, the box's share per GPU) and one core,
+    each gated byte for byte against the GPU's output first:
+      value   RS(6,3) encode of the first 64 MiB of each 256 MiB shard
+              (``seconds`` all-core, a third of that on one core);
+      configs XOR 4 x 64 MiB (the whole config), the 3-erasure decode over
+              the same 64 MiB samples of the survivors, and the sampled
+              stripes of configs 4 and 5 (``batched_cpu``, timed by
+              batched_configs while their host bytes exist)."""
     import numpy as np
     import oracle
     sample = [s[: 64 * MiB] for s in shards_np]
     coeff = oracle.cauchy(k, m)
     outs = [np.empty(64 * MiB, np.uint8) for _ in range(m)]
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    cores = cpu_cores()
     oracle.fast_rs_encode(coeff, sample, outs, nthreads=cores)
     for i in range(m):
         if not np.array_equal(gpu_parity[i][: 64 * MiB].cpu().numpy(), outs[i]):
             raise AssertionError(f"GPU parity {i} differs from the CPU encoder")
-    if not np.array_equal(gpu_xor.cpu().numpy(), oracle.fast_xor_encode(xor_host, nthreads=cores)):
+    xor_cpu = oracle.fast_xor_encode(xor_host, nthreads=cores)
+    if not np.array_equal(gpu_xor.cpu().numpy(), xor_cpu):
         raise AssertionError("GPU XOR parity differs from the CPU encoder")
-
-    def rate(threads, budget):
-        oracle.fast_rs_encode(coeff, sample, outs, nthreads=threads)  # warm
-        n, t0 = 0, time.perf_counter()
-        while True:
-            oracle.fast_rs_encode(coeff, sample, outs, nthreads=threads)
-            n += 1
-            dt = time.perf_counter() - t0
-            if dt >= budget:
-                return n * k * 64 * MiB / dt / 1e9, n
     # correctness gate: the baseline must reproduce the scalar oracle
     ref = oracle.rs_encode(coeff, [s[: 1 * MiB] for s in sample])
     chk = oracle.fast_rs_encode(coeff, [s[: 1 * MiB] for s in sample], nthreads=cores)
     if not all(np.array_equal(a, b) for a, b in zip(ref, chk)):
         raise AssertionError("CPU baseline disagrees with the scalar oracle")
-    all_gbs, n_all = rate(cores, seconds)
-    one_gbs, n_one = rate(1, seconds / 3)
+    enc = cpu_rates(lambda t: oracle.fast_rs_encode(coeff, sample, outs, nthreads=t),
+                    k * 64 * MiB, seconds)
+    configs = {}
+    xout = np.empty_like(xor_cpu)
+    configs["xor_4x64MiB"] = {
+        **cpu_rates(lambda t: oracle.fast_xor_encode(xor_host, out=xout, nthreads=t),
+                    sum(x.size for x in xor_host), seconds / 5),
+        "sample": "the whole config, byte-identical to the GPU parity"}
+    # the decode: the GPU recovered the lost shards bit-exactly (checked in
+    # main); here the same rows rebuild the 64 MiB samples of the lost shards
+    codeword = sample + outs
+    surv, rows = oracle.decode_matrix(coeff, k, m, lost)
+    rec = [np.empty(64 * MiB, np.uint8) for _ in lost]
+    oracle.fast_rs_encode(rows, [codeword[g] for g in surv], rec, nthreads=cores)
+    if not all(np.array_equal(r, codeword[g]) for r, g in zip(rec, lost)):
+        raise AssertionError("CPU decode does not rebuild the lost shards")
+    configs["rs63_decode_3_erasures"] = {
+        **cpu_rates(lambda t: oracle.fast_rs_encode(rows, [codeword[g] for g in surv], rec,
+                                                    nthreads=t), k * 64 * MiB, seconds / 5),
+        "sample": f"lost {list(lost)}: the first 64 MiB of each of the 6 survivors, "
+                  "rebuilding the lost shards byte for byte"}
+    configs.update(batched_cpu)
     return {
-        "value": round(all_gbs, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+        "value": enc["all_cores_GBps"], "unit": "GB/s", "cores": cores, "kind": "port",
         "sample": (f"RS(6,3) encode of the first 64 MiB of each of the 6 shards "
-                   f"(384 MiB data), repeated {n_all}x over ~{seconds:.0f} s with "
-                   f"{cores} threads; repo CPU encoder ({oracle.fast_isa()}), the "
-                   f"reference ships none"),
-        "one_core_GBps": round(one_gbs, 2),
+                   f"(384 MiB data), repeated over ~{seconds:.0f} s with {cores} threads; "
+                   f"repo CPU encoder ({oracle.fast_isa()}), the reference ships none"),
+        "one_core_GBps": enc["one_core_GBps"],
         "isa": oracle.fast_isa(),
+        "configs": configs,
     }
 
 
-def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad") -> dict:
+def cpu_cores() -> int:
+    """Threads of the CPU baseline: the usable cores, at most 16 (the box's
+    share per GPU)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_rates(run, data_bytes: int, seconds: float) -> dict:
+    """all-core and one-core GB/s of data for ``run(threads)``, each repeated
+    for about ``seconds`` (one core: a third of that) after a warm call."""
+    cores = cpu_cores()
+    out = {}
+    for key, threads, budget in (("all_cores_GBps", cores, seconds),
+                                 ("one_core_GBps", 1, seconds / 3)):
+        run(threads)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            run(threads)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget:
+                break
+        out[key] = round(n * data_bytes / dt / 1e9, 2)
+    out["cores"] = cores
+    return out
+
+
+def cpu_batched(coeff, hptr, hlen, stripes, unit: int, gpu_parity, seconds: float,
+                what: str) -> dict:
+    """The repo's SIMD CPU encoder (ecfast_encode_batched) over the given
+    stripes of a batched layout, through host descriptors of the same bytes
+    the GPU coded; gated byte for byte against the GPU's parity of those
+    stripes (``gpu_parity``: [len(stripes), m, unit] host array)."""
+    import numpy as np
+    import oracle
+    m = coeff.shape[0]
+    dp = np.ascontiguousarray(hptr[stripes])
+    dl = np.ascontiguousarray(hlen[stripes])
+    par = np.empty((len(stripes), m, unit), np.uint8)
+    pp = (np.uint64(par.ctypes.data) +
+          np.arange(len(stripes) * m, dtype=np.uint64).reshape(len(stripes), m) * np.uint64(unit))
+    run = lambda threads: oracle.fast_encode_batched(coeff, dp, dl, pp, unit, nthreads=threads)
+    run(cpu_cores())
+    if not np.array_equal(par, gpu_parity):
+        raise AssertionError(f"{what}: GPU parity differs from the CPU encoder")
+    res = cpu_rates(run, int(dl.sum()), seconds)
+    res["sample"] = (f"{len(stripes)} stripes ({int(dl.sum()) / 1e6:.0f} MB of data), "
+                     "byte-identical to the GPU parity")
+    return res
+
+
+def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: float = 0.0) -> dict:
     """Configs 4 and 5 through the batched stripe launcher: data GB/s of one
     launch (HIP events) and HBM traffic GB/s, with product-only checks (a
-    decode round trip; update == full re-encode)."""
+    decode round trip; update == full re-encode).  The bytes are drawn on
+    the host (numpy, seeded, on the box's cores) and uploaded; with
+    ``cpu_seconds`` the repo's CPU encoder is timed on sampled stripes of the
+    same host bytes (key "cpu")."""
     import numpy as np
     import torch
-    out = {}
+    from megatron_lm_amd.layout import stripe_descriptors
+    out, cpu = {}, {}
     # config 4: one rank's 20.8 GB buffer, RS(8,2), 4 MiB units (620 stripes)
-    buf = synth.gpt_rank_buffer(dev, seed)
+    t0 = time.perf_counter()
+    host = synth.gpt_rank_buffer_host(seed)
+    t1 = time.perf_counter()
+    buf = torch.from_numpy(host).to(dev)
+    torch.cuda.synchronize()
+    log(f"config 4: {host.size / 1e9:.2f} GB drawn in {t1 - t0:.1f} s, uploaded in "
+        f"{time.perf_counter() - t1:.1f} s")
     lay = pkg.StripeLayout([buf], 8, 2, 4 * MiB)
     par = lay.alloc_parity()
     w, e = timed(lambda: lay.encode(par), 10, 2)
+    if cpu_seconds:
+        _, hptr, hlen = stripe_descriptors([host.ctypes.data], [host.size], 8, 4 * MiB)
+        sample = list(range(16)) + [lay.n_stripes - 1]
+        cpu["rs82_20.8GB"] = {**cpu_batched(lay.coeff, hptr, hlen, sample, 4 * MiB,
+                                            par[sample].cpu().numpy(), cpu_seconds,
+                                            "config 4"),
+                              "gpu_GBps": round(lay.data_bytes / (w * 1e-3) / 1e9, 1)}
+        log(f"config 4 CPU: {cpu['rs82_20.8GB']}")
+    del host
     keep = (lay.unit_view(3).clone(), par[0, 1].clone())
     lay.unit_view(3).zero_()
     par[0, 1].zero_()
@@ -162,10 +248,20 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad") -> dict:
     torch.cuda.empty_cache()
 
     # config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units, 1% update
-    tensors = ragged_tensors(synth, dev, seed)
+    tensors, views = ragged_tensors(synth, dev, seed, with_host=True)
     lay = pkg.StripeLayout(tensors, 12, 4, 64 << 10)
     par = lay.alloc_parity()
     w, e = timed(lambda: lay.encode(par), 10, 2)
+    if cpu_seconds:
+        _, hptr, hlen = stripe_descriptors([v.ctypes.data for v in views],
+                                           [v.size for v in views], 12, 64 << 10)
+        sample = list(range(0, lay.n_stripes, max(1, lay.n_stripes // 2000)))
+        cpu["rs124_ragged"] = {**cpu_batched(lay.coeff, hptr, hlen, sample, 64 << 10,
+                                             par[sample].cpu().numpy(), cpu_seconds,
+                                             "config 5"),
+                               "gpu_GBps": round(lay.data_bytes / (w * 1e-3) / 1e9, 1)}
+        log(f"config 5 CPU: {cpu['rs124_ragged']}")
+    del views
     out["rs124_ragged_GBps"] = round(lay.data_bytes / (w * 1e-3) / 1e9, 1)
     out["rs124_ragged_traffic_GBps"] = round((lay.data_bytes + par.numel()) / (e * 1e-3) / 1e9, 1)
     out["rs124_ragged_data_GB"] = round(lay.data_bytes / 1e9, 2)
@@ -204,6 +300,8 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad") -> dict:
     out.update(checkpoint_snapshot(pkg, tensors, gemm))
     del tensors
     torch.cuda.empty_cache()
+    if cpu:
+        out["cpu"] = cpu
     return out
 
 
@@ -213,7 +311,8 @@ def checkpoint_staging(pkg, tensors) -> dict:
     memory through 1 GiB pinned chunks, and back: k slices with two data
     positions missing to rebuilt tensors.  Data GB/s over wall time.  The
     first encode writes a fresh host array (page faults and zeroing on first
-    touch: the "cold" rate); the next ones reuse it, as repeated saves do.
+    touch: the "cold" rate); each result is handed back with release() and
+    the next encode reuses its array, as the manager's repeated saves do.
     The transfers share the host's PCIe and memory with other tenants, so the
     median of three calls is reported for each direction."""
     import statistics
@@ -225,17 +324,16 @@ def checkpoint_staging(pkg, tensors) -> dict:
     try:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        codec.encode(tensors)                # result dropped: the host array is free again
+        _, slices = codec.encode(tensors)
         t_cold = time.perf_counter() - t0
-        t_enc, keep = [], None
+        t_enc = []
         for _ in range(3):
-            keep = None                      # the last call's slices free the host array
+            codec.release(slices)            # the next encode writes into the same array
             t0 = time.perf_counter()
             meta, slices = codec.encode(tensors)
             t_enc.append(time.perf_counter() - t0)
-            keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
-            keep = dict(list(sorted(keep.items()))[:12])
-            del slices
+        keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
+        keep = dict(list(sorted(keep.items()))[:12])
         t_dec = []
         for _ in range(3):
             t0 = time.perf_counter()
@@ -247,6 +345,7 @@ def checkpoint_staging(pkg, tensors) -> dict:
                 raise AssertionError("checkpoint decode did not rebuild the tensors")
             del rebuilt
         del keep
+        codec.release(slices)
         log(f"staging calls: encode {[round(t, 3) for t in t_enc]} s (cold {t_cold:.3f}), "
             f"decode {[round(t, 3) for t in t_dec]} s")
         res = {"ckpt_encode_to_host_GBps": round(nbytes / statistics.median(t_enc) / 1e9, 1),
@@ -351,7 +450,7 @@ def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
     nbytes = sum(t.numel() * t.element_size() for t in tensors)
     try:
         g_alone = gemm.ms_alone()
-        codec.snapshot(tensors).result()         # warm: pinned buffers, host array
+        codec.release(codec.snapshot(tensors).result()[1])   # warm: pinned buffers, host array
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         pending = codec.snapshot(tensors)
@@ -374,6 +473,8 @@ def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
                 not all(np.array_equal(a[:64 << 20], b[:64 << 20])
                         for a, b in zip(slices[:12], again[:12])):
             raise AssertionError("snapshot slices differ from the synchronous encode")
+        codec.release(again)
+        codec.release(slices)
         del again, slices
         res = {"ckpt_snapshot_stall_ms": round(t_stall * 1e3, 2),
                "ckpt_snapshot_stall_data_GBps": round(nbytes / t_stall / 1e9, 1),
@@ -426,17 +527,47 @@ def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
             "encode_frac_of_mix_bound": round(enc_traffic_gbs / bound, 4)}
 
 
-def ragged_tensors(synth, dev, seed: int):
-    """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB)."""
+def small_shards(pkg, dev) -> dict:
+    """RS(6,3) over small shards, where the per-call host work competes with
+    the kernel: back-to-back calls through matvec (checks and ctypes arrays
+    built on every call) and through a ShardPlan (built once, one foreign
+    call per launch).  HBM traffic GB/s over wall time, 9 shards per call."""
     import torch
-    sizes, kinds = synth.ragged_sizes(seed)
-    tensors = []
-    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
-        dt = torch.bfloat16 if kind == 0 else torch.float32
-        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
-        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
-        tensors.append(t)
-    return tensors
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    coeff = pkg.cauchy_matrix(6, 3)
+    out = {}
+    for mib in (1, 4):
+        n = mib * MiB
+        data = [torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g)
+                for _ in range(6)]
+        par = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(3)]
+        plan = pkg.ShardPlan(coeff, data, out=par)
+        calls = 400
+        w_eager, _ = timed(lambda: pkg.matvec(coeff, data, out=par), calls, 50)
+        w_plan, _ = timed(plan, calls, 50)
+        out[f"rs63_{mib}MiB_eager_traffic_GBps"] = round(9 * n / (w_eager * 1e-3) / 1e9, 1)
+        out[f"rs63_{mib}MiB_plan_traffic_GBps"] = round(9 * n / (w_plan * 1e-3) / 1e9, 1)
+        out[f"rs63_{mib}MiB_eager_us_per_call"] = round(w_eager * 1e3, 2)
+        out[f"rs63_{mib}MiB_plan_us_per_call"] = round(w_plan * 1e3, 2)
+    log(f"small shards: {out}")
+    return out
+
+
+def ragged_tensors(synth, dev, seed: int, with_host: bool = False):
+    """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB),
+    drawn on the host (synth.ragged_host) and uploaded one by one; with
+    ``with_host`` also their host byte arrays."""
+    import torch
+    t0 = time.perf_counter()
+    block, views, kinds = synth.ragged_host(seed)
+    t1 = time.perf_counter()
+    tensors = [torch.from_numpy(v).to(dev).view(torch.bfloat16 if kd == 0 else torch.float32)
+               for v, kd in zip(views, kinds.tolist())]
+    torch.cuda.synchronize()
+    log(f"config 5: {block.size / 1e9:.2f} GB drawn in {t1 - t0:.1f} s, uploaded in "
+        f"{time.perf_counter() - t1:.1f} s")
+    return (tensors, views) if with_host else tensors
 
 
 def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
@@ -539,21 +670,21 @@ def training_with_checkpoints(pkg, dev, steps: int = 40, every: int = 10) -> dic
     pending = []
 
     def run(save):
-        codec.snapshot(state()).result()          # warm: host array, pinned buffers
+        codec.release(codec.snapshot(state()).result()[1])  # warm: host array, pinned buffers
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(steps):
             step()
             if save == "sync" and (i + 1) % every == 0:
-                codec.encode(state())
+                codec.release(codec.encode(state())[1])   # slices written: array reused
             elif save == "snapshot" and (i + 1) % every == 0:
-                if pending:   # the previous save's slices are written by now: drop
-                    pending.pop().result()   # them, so that their host array is reused
+                if pending:   # the previous save's slices are written by now: hand
+                    codec.release(pending.pop().result()[1])   # their array back for reuse
                 pending.append(codec.snapshot(state()))
         torch.cuda.synchronize()
         t = time.perf_counter() - t0
         for p in pending:
-            p.result()
+            codec.release(p.result()[1])
         pending.clear()
         return t * 1e3 / steps
 
@@ -745,9 +876,12 @@ def main() -> int:
         raise AssertionError("XOR parity does not reproduce the shards")
     xor_gbs = 4 * 64 * MiB / (xwall * 1e-3) / 1e9
     log(f"XOR(4) {xor_gbs:.1f} GB/s data")
+    small = small_shards(pkg, dev)
 
     gemm = GemmLoad(dev)
-    batched = {} if args.no_batched else batched_configs(pkg, synth, dev, args.seed, gemm)
+    batched = {} if args.no_batched else batched_configs(
+        pkg, synth, dev, args.seed, gemm, 0.0 if args.no_cpu_baseline else args.cpu_seconds / 5)
+    batched_cpu = batched.pop("cpu", {})
     log("encode on a side stream vs bf16 GEMMs")
     over = overlap_with_training(pkg, dev, data, parity, coeff, gemm)
     del gemm
@@ -771,7 +905,9 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline")
-        cpu = cpu_baseline(host, k, m, args.cpu_seconds, parity, xh, xp)
+        cpu = cpu_baseline(host, k, m, args.cpu_seconds, parity, xh, xp, lost, batched_cpu)
+        cpu["configs"]["xor_4x64MiB"]["gpu_GBps"] = round(xor_gbs, 1)
+        cpu["configs"]["rs63_decode_3_erasures"]["gpu_GBps"] = round(dec_gbs, 1)
         log(f"CPU {cpu['value']} GB/s on {cpu['cores']} cores, {cpu['one_core_GBps']} GB/s on 1")
 
     result = {
@@ -809,6 +945,7 @@ def main() -> int:
             "decode_GBps": round(dec_gbs, 2), "decode_lost": lost,
             "decode_kernel_us": round(dev_ms * 1e3, 2),
             "xor_4x64MiB_GBps": round(xor_gbs, 2), "xor_kernel_us": round(xev * 1e3, 2),
+            **small,
             **batched,
             **over,
             "copy_ceiling_GBps": round(copy_gbs, 1),

@@ -7,7 +7,8 @@ generator), erasure reconstruction and a batched ragged-stripe launcher with
 incremental parity update.
 
 Modules:
-  codec    equal-size shards: xor_encode, rs_encode, reconstruct, host algebra
+  codec    equal-size shards: xor_encode, rs_encode, reconstruct, ShardPlan (a
+           prepared call for repeated launches), host algebra
   layout   ragged tensor lists -> units -> stripes; batched encode/decode/update
   api      the drop-in entry points encode / decode / update
   checkpoint  ECLocalCheckpointManager + ErasureCodedStrategy (the repl_strategy slot)
@@ -15,13 +16,13 @@ Modules:
 """
 from . import _lib
 from ._lib import ECError, ECLibraryMissing, SingularError
-from .codec import (cauchy_matrix, decode_matrix, gf_inv, gf_invert, gf_mul, matvec,
+from .codec import (ShardPlan, cauchy_matrix, decode_matrix, gf_inv, gf_invert, gf_mul, matvec,
                     reconstruct, rs_encode, side_stream, xor_encode)
 from .layout import StripeLayout
 from .api import ParitySet, decode, encode, update
 
 __all__ = [
-    "ECError", "ECLibraryMissing", "SingularError", "cauchy_matrix", "decode_matrix",
+    "ECError", "ECLibraryMissing", "SingularError", "ShardPlan", "cauchy_matrix", "decode_matrix",
     "gf_inv", "gf_invert", "gf_mul", "matvec", "reconstruct", "rs_encode", "side_stream",
     "xor_encode",
     "StripeLayout", "ParitySet", "encode", "decode", "update",

@@ -17,12 +17,14 @@ This module fills the reserved choice:
 * ``validate_erasure_coding_args(args)`` applies the reference's rules to
   ``in_memory`` (a local directory is required, as for ``local``) and checks
   the code's shape;
-* ``build_checkpointing_context(args, group)`` returns the
+* ``build_checkpointing_context(args, group, gloo_group)`` returns the
   ``checkpointing_context`` dict that training.py:833-838 builds, with an
-  ``ECLocalCheckpointManager`` whose strategy places slices ``--ec-jump``
-  ranks apart.  ``--ec-jump`` has the meaning of ``--replication-jump``; it is
-  a flag of its own because the reference's validation clears
-  ``replication_jump`` when ``--replication`` is off (arguments.py:1054-1056).
+  ``ECLocalCheckpointManager`` whose strategy places the slices of rank n on
+  the coding-group members at least n + J, n + 2J, ... global ranks apart
+  (J = ``--ec-jump``).  ``--ec-jump`` has the meaning of
+  ``--replication-jump``; it is a flag of its own because the reference's
+  validation clears ``replication_jump`` when ``--replication`` is off
+  (arguments.py:1054-1056).
 
 Data-parallel ranks are the coding group, as replication uses them.
 """
@@ -72,9 +74,10 @@ def add_erasure_coding_args(parser: argparse.ArgumentParser) -> argparse.Argumen
                             "hold training only for that, and stage, exchange and write the "
                             "slices from a background thread.")
     group.add_argument("--ec-jump", type=int, default=None,
-                       help="Spacing J between the ranks holding one rank's k + m slices "
-                            "(rank n, n + J, n + 2J, ...), as --replication-jump; set it to "
-                            "the ranks per node to survive whole-node losses. Default 1.")
+                       help="Spacing J in global ranks between the ranks holding one rank's "
+                            "k + m slices (rank n, then the coding-group members at least "
+                            "n + J, n + 2J, ... away), as --replication-jump; set it to the "
+                            "ranks per node to survive whole-node losses. Default 1.")
     return parser
 
 
@@ -99,18 +102,22 @@ def validate_erasure_coding_args(args) -> None:
     assert jump is None or jump >= 1, f"--ec-jump must be positive, got {jump}"
 
 
-def build_checkpointing_context(args, group=None, codec=None) -> dict:
+def build_checkpointing_context(args, group=None, codec=None, gloo_group=None) -> dict:
     """``checkpointing_context`` for ``--non-persistent-ckpt-type in_memory``
     (the erasure-coded counterpart of training.py:806-838); an empty dict for
     any other type.  ``group`` is the coding group (the data-parallel group
-    with context parallelism in Megatron); None means the default group."""
+    with context parallelism in Megatron, megatron/core/parallel_state.py:1240);
+    None means the default group.  ``gloo_group`` is its gloo twin
+    (``get_data_parallel_group_gloo(with_context_parallel=True)``,
+    parallel_state.py:1258), which the slice exchange runs on; without it the
+    strategy builds a private gloo group over the coding group's ranks."""
     if args.non_persistent_ckpt_type != IN_MEMORY:
         return {}
     validate_erasure_coding_args(args)
     from .checkpoint import ECLocalCheckpointManager, ErasureCodedStrategy
-    strategy = ErasureCodedStrategy(args.ec_data_units, args.ec_parity_units,
-                                    args.ec_unit_bytes, group=group, codec=codec,
-                                    jump=args.ec_jump or 1)
+    strategy = ErasureCodedStrategy.from_ec_params(
+        args.ec_data_units, args.ec_parity_units, args.ec_unit_bytes, jump=args.ec_jump or 1,
+        group=group, gloo_group=gloo_group, codec=codec)
     return {"local_checkpoint_manager":
             ECLocalCheckpointManager(args.non_persistent_local_ckpt_dir, strategy,
                                      stage_in_background=args.ec_stage_in_background)}

@@ -21,22 +21,26 @@ each rank's ordered tensor list:
 
 * the rank's tensors are cut into stripes of k units of ``unit_bytes``
   (``StripeLayout``) and m parity units are computed on the GPU;
-* codeword position p (data 0..k-1, parity k..k+m-1) of rank r's stripes is
-  a *slice* of n_stripes * unit_bytes bytes held by group rank
-  (r + p * jump) mod G, so the storage of any m ranks can be lost and every
-  rank still decodes (the k + m holders must be distinct:
-  G / gcd(jump, G) >= k + m);
-* ``jump`` has the meaning of the reference's ``--replication-jump``
-  (megatron/training/arguments.py:2425-2429: copies of rank n go to n + J,
-  n + 2J, ...).  With ranks numbered node-major and jump = ranks per node,
-  the k + m slices of a rank sit on k + m different nodes, so losing up to m
-  whole nodes still loads;
+* codeword position p (data 0..k-1, parity k..k+m-1) of the stripes of the
+  rank at index i of the group's rank list is a *slice* of
+  n_stripes * unit_bytes bytes held by the rank at index (i + p * jump) mod G,
+  so the storage of any m ranks can be lost and every rank still decodes (the
+  k + m holders must be distinct: G / gcd(jump, G) >= k + m);
+* ``ErasureCodedStrategy.from_ec_params`` takes ``jump`` with the meaning of
+  the reference's ``--replication-jump`` (megatron/training/arguments.py:2425-2429:
+  copies of rank n go to n + J, n + 2J, ... in global ranks) and converts it
+  to a spacing of group members (``index_jump``).  With ranks numbered
+  node-major and J = ranks per node, the k + m slices of a rank sit on k + m
+  different nodes, so losing up to m whole nodes still loads;
 * storage is (k + m) / k of the data per rank, and a save moves
   (k + m - 1) / k of it over the network.  Replication with factor F stores
   F times the data and tolerates F - 1 losses.
 
-Slices and inventories are exchanged over the group's ``torch.distributed``
-backend as CPU tensors (send/recv, all_gather), and files are written as a
+Slices and inventories are exchanged as CPU tensors (send/recv, all_gather)
+over a gloo group with the coding group's ranks (``comm_group``: the coding
+group itself when it is gloo, a given gloo twin, or a private gloo group built
+from the coding group's ranks, since the reference's data-parallel group is
+NCCL), and files are written as a
 JSON header plus raw bytes.  The one serialized object is the hollow state of
 a ``MCoreTensorAwareStateDict`` (its non-tensor part, torch.save), stored
 with the slices so that ``load`` returns the object it was given, as the
@@ -51,7 +55,6 @@ import io
 import json
 import os
 import re
-import sys
 import threading
 import time
 import weakref
@@ -188,10 +191,12 @@ class GpuSliceCodec:
     (k, stripes, unit_bytes) block when it fits, else chunks, and moves the
     slices up with ``ec_stage_to_device``.
 
-    The codec keeps the host array of its last encode and writes the next
-    encode of the same shape into it once no slice of it is referenced any
-    more (the slices are views, so they hold the array): a fresh array costs
-    the kernel's page faults and zeroing on first touch, which on a 27 GB
+    The slices own their host array (they are views of it): the codec keeps
+    no reference to an array it handed out, so nothing the caller holds,
+    even only by address, is written again behind its back.  A caller done
+    with the slices hands the array back with ``release(slices)``, and the
+    next encode of the same shape writes into it: a fresh array costs the
+    kernel's page faults and zeroing on first touch, which on a 27 GB
     checkpoint halves the staging rate.
 
     Encode, per chunk: one launch writes the parity units into the device
@@ -219,20 +224,34 @@ class GpuSliceCodec:
         self.chunk_bytes = chunk_bytes
         self.snapshot_bytes = snapshot_bytes
         self.stage_threads = 8   # host threads of a snapshot's background staging
-        self._host: Optional[np.ndarray] = None
+        self._free: Optional[np.ndarray] = None   # released by the caller, reusable
         self._host_lock = threading.Lock()
 
     def _host_out(self, shape: Tuple[int, int]) -> np.ndarray:
-        """The previous encode's host array when it has this shape and no
-        view of it is alive, else a new one (which replaces it)."""
+        """The released host array when it has this shape, else a new one.
+        A released array of another shape is dropped."""
         with self._host_lock:
-            buf = self._host
-            # references: self._host, buf, getrefcount's argument; a live slice adds one
-            if buf is not None and buf.shape == shape and sys.getrefcount(buf) == 3:
-                return buf
-            self._host = buf = None
-            self._host = np.empty(shape, np.uint8)
-            return self._host
+            buf, self._free = self._free, None
+        if buf is not None and buf.shape == shape:
+            return buf
+        del buf
+        return np.empty(shape, np.uint8)
+
+    def release(self, slices: Sequence[np.ndarray]) -> None:
+        """Hand back the host array of the k + m slices an ``encode`` or a
+        ``snapshot`` returned, for the next encode of the same shape to write
+        into.  The caller must not use the slices (or their memory) after
+        this.  ValueError for anything that is not one encode's slices."""
+        slices = list(slices)
+        if not slices:
+            return
+        base = slices[0].base
+        if (not isinstance(base, np.ndarray) or base.ndim != 2 or base.dtype != np.uint8
+                or len(slices) != base.shape[0]
+                or any(sl.base is not base or sl.size != base.shape[1] for sl in slices)):
+            raise ValueError("release() takes the slices of one encode or snapshot")
+        with self._host_lock:
+            self._free = base
 
     def _chunk_stripes(self, n_stripes: int, rows: int) -> int:
         return max(1, min(n_stripes, self.chunk_bytes // (rows * self.unit_bytes)))
@@ -546,34 +565,135 @@ class GpuSliceCodec:
 
 # -------------------------------------------------------------- strategy --
 
+def _is_gloo(group) -> bool:
+    """Whether CPU tensors in collectives on ``group`` (None: the default
+    group) go to gloo: a gloo group, or a multi-device group with a gloo
+    part ("cpu:gloo,cuda:nccl")."""
+    try:
+        return "gloo" in str(dist.get_backend(group)).lower()
+    except (RuntimeError, ValueError):
+        return False
+
+
+# One private gloo group per rank set and default group, created by the
+# members only (use_local_synchronization): its name is a hash of the ranks,
+# so a second group over the same ranks cannot be created in this process.
+_private_gloo: Dict[Tuple[int, ...], Tuple[object, object]] = {}
+_private_gloo_lock = threading.Lock()
+
+
+def private_gloo_group(ranks: Sequence[int]):
+    """A gloo group over ``ranks`` that only the erasure-coded checkpoint
+    code uses, created on first use by the members (collective over them
+    only) and kept for the life of the default group.  Raises
+    CheckpointingException if gloo cannot build it."""
+    key = tuple(sorted(int(r) for r in ranks))
+    world = dist.group.WORLD
+    with _private_gloo_lock:
+        hit = _private_gloo.get(key)
+        if hit is not None and hit[0] is world:
+            return hit[1]
+        try:
+            g = dist.new_group(ranks=list(key), backend="gloo", use_local_synchronization=True)
+        except (RuntimeError, ValueError) as e:
+            raise CheckpointingException(
+                f"cannot create a gloo group over ranks {list(key)} for the checkpoint "
+                f"exchange: {e}") from e
+        _private_gloo[key] = (world, g)
+        return g
+
+
+def index_jump(ranks: Sequence[int], jump: int) -> int:
+    """The group-index spacing that puts consecutive holders at least
+    ``jump`` global ranks apart, for the reference's ``--replication-jump``
+    (megatron/training/arguments.py:2425-2429: copies of rank n go to n + J,
+    n + 2J, ...) applied to a coding group whose members are evenly spaced
+    (a data-parallel group: stride TP x PP, or 1).  ceil(jump / stride).
+    Raises CheckpointingException for a jump above 1 on a group whose ranks
+    are not evenly spaced."""
+    if jump < 1:
+        raise ValueError("jump must be positive")
+    r = sorted(int(x) for x in ranks)
+    if jump == 1 or len(r) < 2:
+        return 1
+    strides = {b - a for a, b in zip(r, r[1:])}
+    if len(strides) != 1:
+        raise CheckpointingException(
+            f"a global-rank jump of {jump} needs evenly spaced group ranks, got {r}; "
+            "pass a group-index jump to ErasureCodedStrategy instead")
+    s = strides.pop()
+    return -(-jump // s)
+
+
 class ErasureCodedStrategy:
-    """(k, m) erasure code over each rank's tensors; slice p of rank r is
-    held by group rank (r + p * jump) mod G (see module docstring)."""
+    """(k, m) erasure code over each rank's tensors; slice p of the rank at
+    index i of the group's rank list is held by the rank at index
+    (i + p * jump) mod G (see module docstring).  ``jump`` here counts group
+    members; ``from_ec_params`` takes the reference's global-rank spacing.
+
+    ``group`` is the coding group (in Megatron the data-parallel group with
+    context parallelism, an NCCL group).  The exchange moves CPU tensors, so
+    every collective runs on a gloo group over the same ranks: ``gloo_group``
+    when given (Megatron's ``get_data_parallel_group_gloo(
+    with_context_parallel=True)``, megatron/core/parallel_state.py:1258), else
+    ``group`` itself when its backend takes CPU tensors (gloo), else a
+    private gloo group built from ``group``'s ranks on first use
+    (``private_gloo_group``)."""
 
     def __init__(self, k: int, m: int, unit_bytes: int = 4 << 20,
-                 group: Optional[dist.ProcessGroup] = None, codec=None, jump: int = 1):
+                 group: Optional[dist.ProcessGroup] = None, codec=None, jump: int = 1,
+                 gloo_group: Optional[dist.ProcessGroup] = None):
         if k < 1 or m < 1:
             raise ValueError("k and m must be positive")
         if jump < 1:
             raise ValueError("jump must be positive")
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.group, self.jump = group, jump
+        self.gloo_group = gloo_group
+        self._comm: Optional[Tuple[object]] = None
         self.codec = codec if codec is not None else GpuSliceCodec(k, m, unit_bytes)
 
     @classmethod
     def from_ec_params(cls, k: int, m: int, unit_bytes: int = 4 << 20, jump: int = 1,
-                       group: Optional[dist.ProcessGroup] = None) -> "ErasureCodedStrategy":
+                       group: Optional[dist.ProcessGroup] = None,
+                       gloo_group: Optional[dist.ProcessGroup] = None,
+                       codec=None) -> "ErasureCodedStrategy":
         """Counterpart of the reference's
         ``CliqueReplicationStrategy.from_replication_params(jump, factor)``
         (megatron/training/training.py:826-828): the code's shape replaces the
-        replication factor, ``jump`` keeps its meaning."""
-        return cls(k, m, unit_bytes, group=group, jump=jump)
+        replication factor, and ``jump`` has the meaning of
+        ``--replication-jump``, a spacing in global ranks, converted to a
+        spacing in the group's members by ``index_jump``.  With jump = ranks
+        per node (ranks numbered node-major) consecutive holders of a rank's
+        slices sit on different nodes."""
+        members = dist.get_process_group_ranks(group) if group is not None \
+            else list(range(dist.get_world_size()))
+        return cls(k, m, unit_bytes, group=group, codec=codec, jump=index_jump(members, jump),
+                   gloo_group=gloo_group)
 
     # group helpers
     def ranks(self) -> List[int]:
         if self.group is None:
             return list(range(dist.get_world_size()))
         return dist.get_process_group_ranks(self.group)
+
+    def comm_group(self):
+        """The gloo group every CPU-tensor collective of the manager runs on
+        (None: the default group, when that is gloo).  Resolved once."""
+        if self._comm is None:
+            if self.gloo_group is not None:
+                if not _is_gloo(self.gloo_group):
+                    raise CheckpointingException(
+                        f"gloo_group has backend {dist.get_backend(self.gloo_group)!r}, not gloo")
+                if sorted(dist.get_process_group_ranks(self.gloo_group)) != sorted(self.ranks()):
+                    raise CheckpointingException(
+                        "gloo_group does not have the ranks of the coding group")
+                self._comm = (self.gloo_group,)
+            elif _is_gloo(self.group):
+                self._comm = (self.group,)
+            else:
+                self._comm = (private_gloo_group(self.ranks()),)
+        return self._comm[0]
 
     def holder(self, owner: int, pos: int) -> int:
         r = self.ranks()
@@ -598,7 +718,7 @@ class ErasureCodedStrategy:
         the lists the plan gives it; transfers are ordered by (owner, pos) so
         that both sides agree on tags."""
         me = dist.get_rank()
-        group = self.group if group is None else group
+        group = self.comm_group() if group is None else group
         reqs, recv = [], {}
         for (src, owner, pos, sizes) in sorted(incoming, key=lambda x: (x[1], x[2])):
             if src == me:
@@ -718,12 +838,12 @@ class ECLocalCheckpointManager:
         g = len(st.ranks())
         count = torch.tensor([rows.shape[0]], dtype=torch.int64)
         counts = [torch.empty_like(count) for _ in range(g)]
-        dist.all_gather(counts, count, group=st.group)
+        dist.all_gather(counts, count, group=st.comm_group())
         width = max(1, max(int(c[0]) for c in counts))
         mine = torch.zeros((width, 4), dtype=torch.int64)
         mine[: rows.shape[0]] = torch.from_numpy(rows)
         every = [torch.empty_like(mine) for _ in range(g)]
-        dist.all_gather(every, mine, group=st.group)
+        dist.all_gather(every, mine, group=st.comm_group())
         return [e[: int(c[0])].numpy() for e, c in zip(every, counts)]
 
     # save
@@ -754,7 +874,8 @@ class ECLocalCheckpointManager:
         st.check_group()
         if is_async and self.stage_in_background:
             return self._save_in_background(state, iteration)
-        error, blobs = None, None
+        self._quiesce()
+        error, blobs, slices = None, None, None
         try:
             # .tensors of MCoreTensorAwareStateDict is an iterator: take it once
             tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
@@ -763,14 +884,19 @@ class ECLocalCheckpointManager:
             blobs = self._blobs(meta, slices, hollow, common, iteration)
         except Exception as e:  # noqa: BLE001 - reported collectively below
             error = e
-        received = self._place(blobs, st.group)
+        received = self._place(blobs, st.comm_group())
         if received is None:
+            self._release(slices)
             raise CheckpointingException(
                 f"erasure-coded save of iteration {iteration} failed on some rank") from error
         jobs, expected = self._jobs(iteration, received)
+        del received, blobs
 
         def finalize():
-            self._finish_save(iteration, _files_complete(expected))
+            try:
+                self._finish_save(iteration, _files_complete(expected))
+            finally:   # the files are written (or failed): the host array is free
+                self._release(slices)
 
         self.local_dir.mkdir(parents=True, exist_ok=True)
         if is_async:
@@ -781,6 +907,13 @@ class ECLocalCheckpointManager:
             pass  # finalize() sees the missing files and fails the save everywhere
         finalize()
         return None
+
+    def _release(self, slices) -> None:
+        """Hand an encode's host array back to the codec once the slices are
+        on disk (codecs without ``release`` keep no arrays)."""
+        release = getattr(self.strategy.codec, "release", None)
+        if slices is not None and release is not None:
+            release(slices)
 
     def _blobs(self, meta: dict, slices, hollow: bytes, common: dict,
                iteration: int) -> Dict[int, Tuple[np.ndarray, np.ndarray]]:
@@ -826,13 +959,23 @@ class ECLocalCheckpointManager:
         return jobs, [(path, sum(int(t.numel()) for t in parts)) for path, parts in jobs]
 
     def _background_group(self):
-        """A gloo group over the strategy's ranks for the background thread's
-        collectives, so they never interleave with the caller's on the
-        strategy's group.  Created by the members only."""
+        """The gloo group of the background thread's collectives: the
+        strategy's private group over its ranks, never the caller's group, so
+        that they do not interleave with collectives the caller issues on its
+        own group.  When the strategy's foreground collectives use the same
+        private group (an NCCL coding group), the foreground calls wait for
+        the background thread first (``_quiesce``)."""
         if self._bg_group is None:
-            self._bg_group = dist.new_group(ranks=self.strategy.ranks(), backend="gloo",
-                                            use_local_synchronization=True)
+            self._bg_group = private_gloo_group(self.strategy.ranks())
         return self._bg_group
+
+    def _quiesce(self) -> None:
+        """Wait for the background save in flight, if any: its collectives
+        may use the group the foreground ones are about to use, and a load or
+        a newer save must see the files it writes."""
+        last = self._bg_last
+        if last is not None:
+            last.join()
 
     def _save_in_background(self, state, iteration: int) -> "AsyncSaveRequest":
         st = self.strategy
@@ -847,28 +990,40 @@ class ECLocalCheckpointManager:
         self.local_dir.mkdir(parents=True, exist_ok=True)
         marker = self.local_dir / f".iter_{iteration:07d}.staged"
         marker.unlink(missing_ok=True)
-        prev, box = self._bg_last, {"ok": False, "expected": []}
+        prev, box = self._bg_last, {"ok": False}
 
         def body():
             try:
                 if prev is not None:
                     prev.join()   # one save's collectives at a time, in save order
-                blobs = None
+                blobs, slices = None, None
                 try:
                     if error is not None:
                         raise error
                     meta, slices = pending.result()
                     blobs = self._blobs(meta, slices, hollow, common, iteration)
-                    del slices
                 except Exception as e:  # noqa: BLE001 - reported collectively
                     box["error"] = e
                 received = self._place(blobs, group)
                 if received is not None:
-                    jobs, box["expected"] = self._jobs(iteration, received)
+                    jobs, expected = self._jobs(iteration, received)
                     del received, blobs
-                    _write_slice_files(jobs)
-                    box["ok"] = True
+                    try:
+                        _write_slice_files(jobs)
+                    except OSError as e:
+                        box["error"] = e
+                    del jobs
+                    box["ok"] = _files_complete(expected)
+                self._release(slices)
             except Exception as e:  # noqa: BLE001 - finalize fails the save everywhere
+                box.setdefault("error", e)
+            try:
+                # Agree on success over the background group, in this thread:
+                # every collective of a background save stays in the chain of
+                # background threads, in save order.
+                box["ok"] = self._agree(box["ok"], group)
+            except Exception as e:  # noqa: BLE001
+                box["ok"] = False
                 box.setdefault("error", e)
             finally:
                 tmp = marker.with_name(marker.name + ".tmp")
@@ -882,18 +1037,29 @@ class ECLocalCheckpointManager:
         def finalize():
             thread.join()
             marker.unlink(missing_ok=True)
-            self._finish_save(iteration, box["ok"] and _files_complete(box["expected"]))
+            self._conclude_save(iteration, box["ok"])
 
         return AsyncSaveRequest(_await_marker, (str(marker),), [finalize])
 
-    def _finish_save(self, iteration: int, ok: bool) -> None:
+    @staticmethod
+    def _agree(ok: bool, group) -> bool:
+        """True on every rank of ``group`` iff ``ok`` on every rank."""
         flag = torch.tensor([0 if ok else 1], dtype=torch.int64)
-        dist.all_reduce(flag, group=self.strategy.group)
-        if int(flag[0]):
+        dist.all_reduce(flag, group=group)
+        return int(flag[0]) == 0
+
+    def _finish_save(self, iteration: int, ok: bool) -> None:
+        """Agree on the save over the coding group, then conclude it."""
+        self._conclude_save(iteration, self._agree(ok, self.strategy.comm_group()))
+
+    def _conclude_save(self, iteration: int, agreed: bool) -> None:
+        """After every rank agreed on the outcome: drop the iteration on
+        failure, else the older ones."""
+        if not agreed:
             self._remove(lambda it: it == iteration)
             raise CheckpointingException(f"writing iteration {iteration} failed on some rank")
         self._remove(lambda it: it < iteration)
-        self.latest_iteration = iteration
+        self.latest_iteration = max(self.latest_iteration, iteration)
 
     def _remove(self, pred) -> None:
         if not self.local_dir.is_dir():
@@ -928,6 +1094,7 @@ class ECLocalCheckpointManager:
         return -1, {}
 
     def find_latest(self) -> int:
+        self._quiesce()
         it, _ = self._plan()
         self.latest_iteration = it
         return it
@@ -944,6 +1111,7 @@ class ECLocalCheckpointManager:
         (megatron/training/checkpointing.py:891-899).  Anything else comes
         back as a TensorListState."""
         st = self.strategy
+        self._quiesce()
         it, plan = self._plan()
         if it < 0:
             raise CheckpointingException("no erasure-coded checkpoint can be decoded")
@@ -1055,13 +1223,16 @@ class AsyncSaveRequest(NamedTuple):
         self.finalize_fns.append(fn)
 
     def execute_sync(self) -> None:
-        """Write, synchronise the ranks, then finalize, in the caller."""
+        """Write, then finalize, in the caller.  The reference's version
+        takes a world-wide barrier between the two; here the first finalize
+        function is itself a collective over the coding group (the agreement
+        on the save's success), so ranks of disjoint coding groups finalize
+        independently and no rank outside the group is waited for."""
         if self.async_fn is not None:
             try:
                 self.async_fn(*self.async_fn_args, **self.async_fn_kwargs)
             except OSError:
                 pass  # the finalize function sees the missing files
-        dist.barrier()
         for fn in self.finalize_fns:
             fn()
 

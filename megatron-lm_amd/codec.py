@@ -198,6 +198,59 @@ def matvec(coeff: np.ndarray, shards: Sequence[torch.Tensor], out=None, stream=N
     return outs
 
 
+class ShardPlan:
+    """One flat-shard call (``ec_rs_encode``, ``ec_rs_decode`` or
+    ``ec_xor_encode``) prepared once and launched many times: the checks, the
+    host arrays of device addresses, the coefficient bytes and the stream
+    handle are built here, so a launch is one foreign call.  For callers
+    that code the same shards repeatedly (small shards especially, where
+    matvec's per-call Python work, about 10 us, would otherwise exceed the
+    kernel).
+
+    ``what`` is "ec_rs_encode" (``coeff`` m x k, outputs the parity),
+    "ec_rs_decode" (``coeff`` the e x k rows of ``decode_matrix``, inputs the
+    survivors) or "ec_xor_encode" (``coeff`` ignored, one output).  The plan
+    keeps the tensors alive; it launches on ``stream`` (default: torch's
+    current stream of the shards' device when the plan is made), or on the
+    stream given to the call."""
+
+    def __init__(self, coeff: Optional[np.ndarray], shards: Sequence[torch.Tensor], out=None,
+                 stream=None, what: str = "ec_rs_encode"):
+        if what not in ("ec_rs_encode", "ec_rs_decode", "ec_xor_encode"):
+            raise ValueError(f"unknown entry point {what!r}")
+        ptrs, nbytes = _shards(shards, "shards")
+        device = shards[0].device
+        L = _lib.lib()
+        if what == "ec_xor_encode":
+            k, m = len(ptrs), 1
+            self._coeff = None
+        else:
+            self._coeff = np.ascontiguousarray(coeff, np.uint8)
+            m, k = self._coeff.shape
+            if len(ptrs) != k:
+                raise ValueError(f"coefficient matrix has {k} columns, got {len(ptrs)} shards")
+        self.inputs = list(shards)
+        self.outputs = _outputs(out, m, nbytes, device, "out")
+        self.device, self.what, self.nbytes = device, what, nbytes
+        self._stream = stream_handle(stream, device)
+        self._fn = getattr(L, what)
+        data = _lib.ptr_array(ptrs)
+        if what == "ec_xor_encode":
+            self._head = (data, ctypes.c_int(k), ctypes.c_void_p(self.outputs[0].data_ptr()),
+                          ctypes.c_uint64(nbytes))
+        else:
+            self._head = (_lib.u8ptr(self._coeff), ctypes.c_int(k), ctypes.c_int(m), data,
+                          _lib.ptr_array([t.data_ptr() for t in self.outputs]),
+                          ctypes.c_uint64(nbytes))
+
+    def __call__(self, stream=None) -> List[torch.Tensor]:
+        st = self._stream if stream is None else stream_handle(stream, self.device)
+        status = self._fn(*self._head, st)
+        if status != _lib.EC_OK:
+            _lib.check(status, self.what)
+        return self.outputs
+
+
 def rs_encode(shards: Sequence[torch.Tensor], m: int, coeff: Optional[np.ndarray] = None,
               out=None, stream=None) -> List[torch.Tensor]:
     """m Reed-Solomon parity shards of k equal-size data shards."""

@@ -1,5 +1,6 @@
 // staging.cpp — host side of moving coded checkpoint slices out of HBM
-// (ec_stage_to_host) and back in (ec_stage_to_device).
+// (ec_stage_to_host) and back in (ec_stage_to_device); the host copies are
+// in host_copy.cpp.
 //
 // A background save stages the coded block to host memory while training
 // runs in the same process.  The whole loop (a transfer per chunk and row,
@@ -14,55 +15,11 @@
 // few CUs.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include <string.h>
 
 #include <algorithm>
-#include <thread>
-#include <vector>
 
 #include "ec_mi355.h"
-
-namespace {
-
-// run(t) for t in [0, threads), share 0 on the calling thread and the others
-// on threads of their own.  A thread that cannot be started (the system is
-// out of threads or memory) has its share run on the calling thread, so no
-// C++ exception reaches the C ABI and every started thread is joined.
-template <class F>
-void run_shares(int threads, const F& run) {
-  std::vector<std::thread> pool;
-  int t = 1;
-  try {
-    pool.reserve(threads - 1);
-    for (; t < threads; ++t) pool.emplace_back(run, t);
-  } catch (...) {
-  }
-  for (int u = t; u < threads; ++u) run(u);
-  run(0);
-  for (auto& th : pool) th.join();
-}
-
-// dst[r * dst_pitch + x] = src[r * src_pitch + x] for r < rows, x < width,
-// split by rows (or by column ranges when rows < threads) over `threads`
-// host threads.
-void copy_rect(uint8_t* dst, uint64_t dst_pitch, const uint8_t* src, uint64_t src_pitch,
-               uint32_t rows, uint64_t width, int threads) {
-  // Work items: (row, column begin, column end) with about equal bytes.
-  const uint64_t total = (uint64_t)rows * width;
-  const uint64_t share = (total + threads - 1) / threads;
-  auto run = [&](int t) {
-    uint64_t begin = (uint64_t)t * share, end = std::min(total, begin + share);
-    while (begin < end) {
-      const uint64_t r = begin / width, x = begin % width;
-      const uint64_t n = std::min(end - begin, width - x);
-      memcpy(dst + r * dst_pitch + x, src + r * src_pitch + x, n);
-      begin += n;
-    }
-  };
-  run_shares(threads, run);
-}
-
-}  // namespace
+#include "host_copy.h"
 
 extern "C" {
 
@@ -112,7 +69,7 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
         status = EC_EHIP;
         break;
       }
-      copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
+      ec::copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
     }
   }
   if (status != EC_OK) (void)hipStreamSynchronize(st);  // no transfer outlives the call
@@ -159,16 +116,7 @@ int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row
       break;
     }
     // rows x w bytes, split over the threads by equal shares of bytes
-    const uint64_t total = (uint64_t)rows * w, share = (total + threads - 1) / threads;
-    auto run = [&](int t) {
-      uint64_t b = (uint64_t)t * share, e = std::min(total, b + share);
-      while (b < e) {
-        const uint64_t r = b / w, x = b % w, n = std::min(e - b, w - x);
-        memcpy(pin + r * w + x, h_rows[r] + x0 + x, n);
-        b += n;
-      }
-    };
-    run_shares(threads, run);
+    ec::gather_rows(pin, h_rows, x0, rows, w, threads);
     for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
       if (hipMemcpyAsync(d_dst + (uint64_t)r * dst_pitch + x0, pin + (uint64_t)r * w, w,
                          hipMemcpyHostToDevice, st) != hipSuccess)

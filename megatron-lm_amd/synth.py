@@ -3,14 +3,17 @@
 The bytes stand in for serialized optimizer / parameter state: bf16 params
 N(0, 0.02); fp32 master weights N(0, 0.02), Adam exp_avg N(0, 1e-3) and
 exp_avg_sq |N(0, 1e-6)| (the tensors megatron/core/optimizer/distrib_optimizer.py:860-897
-hands to the checkpoint).  Host generators use numpy ``default_rng(seed)``
-(bf16 by round-to-nearest-even from fp32), so CPU and GPU runs see the same
-bytes.  The multi-GB configurations are generated on the device with a seeded
-torch generator instead (numpy would take minutes); the checks for those read
-the same device bytes back.
+hands to the checkpoint).  Every configuration is generated on the host with
+numpy ``default_rng`` (bf16 by round-to-nearest-even from fp32), so CPU and
+GPU runs see the same bytes.  The multi-GB configurations (the 20.8 GB rank
+buffer, the 3,000 ragged tensors) are drawn in 64 MiB chunks, chunk c of a
+segment from ``default_rng([seed, segment, c])``, on a thread pool: the bytes
+do not depend on the thread count.
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
 from typing import List, Tuple
 
 import numpy as np
@@ -95,6 +98,90 @@ def perturbed_units(seed: int, n_units: int, fraction: float = 0.01) -> np.ndarr
     return np.sort(rng.choice(n_units, n, replace=False))
 
 
+# ------------------------------------------------- multi-GB host buffers --
+
+GEN_CHUNK = 64 * MiB  # bytes per independently seeded chunk
+
+
+def _threads(threads) -> int:
+    return threads or max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def _fill_chunk(out: np.ndarray, c0: int, seed: int, segment: int, std: float, dtype: str,
+                absolute: bool) -> None:
+    """Bytes [c0, c0 + GEN_CHUNK) of the uint8 array ``out``: dtype values
+    N(0, std) (|N| with ``absolute``) from default_rng([seed, segment, chunk])."""
+    c1 = min(out.size, c0 + GEN_CHUNK)
+    rng = np.random.default_rng([seed, segment, c0 // GEN_CHUNK])
+    if dtype == "fp32":
+        x = out[c0:c1].view(np.float32)
+        rng.standard_normal(out=x, dtype=np.float32)
+    else:
+        x = rng.standard_normal((c1 - c0) // 2, dtype=np.float32)
+    x *= np.float32(std)
+    if absolute:
+        np.abs(x, out=x)
+    if dtype == "bf16":
+        out[c0:c1].view(np.uint16)[:] = bf16_bits(x)
+
+
+def fill_normal(segments, seed: int, threads: int = 0) -> None:
+    """Fill each (uint8 array, segment id, std, dtype, absolute) of
+    ``segments`` chunk by chunk on a thread pool (numpy releases the
+    interpreter lock while it draws)."""
+    work = []
+    for out, seg, std, dtype, absolute in segments:
+        width = 2 if dtype == "bf16" else 4
+        if out.size % width:
+            raise ValueError("segment size must be a multiple of the element size")
+        work += [(out, c0, seg, std, dtype, absolute) for c0 in range(0, out.size, GEN_CHUNK)]
+    with ThreadPoolExecutor(_threads(threads)) as ex:
+        for f in [ex.submit(_fill_chunk, o, c0, seed, seg, std, dt, ab)
+                  for o, c0, seg, std, dt, ab in work]:
+            f.result()
+
+
+# Config 4's segments: (share of the 14 bytes per parameter, std, dtype, absolute)
+GPT_SEGMENTS = [(2, 0.02, "bf16", False),   # bf16 params
+                (4, 0.02, "fp32", False),   # fp32 master weights
+                (4, 1e-3, "fp32", False),   # Adam exp_avg
+                (4, 1e-6, "fp32", True)]    # Adam exp_avg_sq
+
+
+def gpt_rank_buffer_host(seed: int, nbytes: int = None, threads: int = 0) -> np.ndarray:
+    """One DP rank's checkpoint buffer for GPT 1.3B as one uint8 host array:
+    the segments bf16 params | fp32 master | fp32 exp_avg | fp32 exp_avg_sq,
+    in the 2:4:4:4 byte ratio of those states, scaled to ``nbytes`` (default
+    the 20.8e9 bytes quoted for this configuration; the exact model,
+    gpt_rank_params() = 1,315,819,520 params at 14 B each, is 18.42e9)."""
+    total = int(20.8e9) if nbytes is None else int(nbytes)
+    unit = total // 14
+    seg = [share * unit - (share * unit) % 4 for share, *_ in GPT_SEGMENTS]
+    buf = np.empty(sum(seg), np.uint8)
+    parts, off = [], 0
+    for i, (n, (_, std, dtype, absolute)) in enumerate(zip(seg, GPT_SEGMENTS)):
+        parts.append((buf[off: off + n], i, std, dtype, absolute))
+        off += n
+    fill_normal(parts, seed, threads)
+    return buf
+
+
+def ragged_host(seed: int, threads: int = 0, n: int = 3000):
+    """Config 5's tensors on the host: (block, views, kinds) where ``views``
+    are the byte arrays of the tensors (sizes from ragged_sizes, back to back
+    in one 64-byte-aligned block), bf16 N(0, 0.02) for kind 0, fp32
+    N(0, 1e-3) for kind 1; tensor i is segment 5000 + i."""
+    sizes, kinds = ragged_sizes(seed, n)
+    starts = np.concatenate([[0], np.cumsum((sizes + 63) // 64 * 64)])
+    raw = np.empty(int(starts[-1]) + 64, np.uint8)
+    lead = (-raw.ctypes.data) % 64
+    block = raw[lead: lead + int(starts[-1])]
+    views = [block[int(a): int(a) + int(sz)] for a, sz in zip(starts[:-1], sizes)]
+    fill_normal([(v, 5000 + i, 0.02 if kd == 0 else 1e-3, "bf16" if kd == 0 else "fp32", False)
+                 for i, (v, kd) in enumerate(zip(views, kinds.tolist()))], seed, threads)
+    return block, views, kinds
+
+
 # ------------------------------------------------------------ device data --
 
 def device_normal_(buf, seed: int, std: float, dtype, absolute: bool = False):
@@ -105,25 +192,4 @@ def device_normal_(buf, seed: int, std: float, dtype, absolute: bool = False):
     buf.normal_(0.0, std, generator=g)
     if absolute:
         buf.abs_()
-    return buf
-
-
-def gpt_rank_buffer(device, seed: int, nbytes: int = None):
-    """One DP rank's checkpoint buffer for GPT 1.3B as one uint8 tensor: the
-    segments bf16 params | fp32 master | fp32 exp_avg | fp32 exp_avg_sq, in
-    the 2:4:4:4 byte ratio of those states, scaled to ``nbytes`` (default the
-    20.8e9 bytes quoted for this configuration; the exact model,
-    gpt_rank_params() = 1,315,819,520 params at 14 B each, is 18.42e9)."""
-    import torch
-    total = int(20.8e9) if nbytes is None else int(nbytes)
-    unit = total // 14
-    seg = [2 * unit, 4 * unit, 4 * unit, 4 * unit]
-    seg = [s - s % 4 for s in seg]
-    buf = torch.empty(sum(seg), dtype=torch.uint8, device=device)
-    off = 0
-    specs = [(torch.bfloat16, 0.02, False), (torch.float32, 0.02, False),
-             (torch.float32, 1e-3, False), (torch.float32, 1e-6, True)]
-    for n, (dt, std, ab) in zip(seg, specs):
-        device_normal_(buf[off: off + n].view(dt), seed + off, std, dt, ab)
-        off += n
     return buf

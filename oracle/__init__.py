@@ -62,6 +62,10 @@ def lib() -> ctypes.CDLL:
         L.ecfast_rs_encode.argtypes = [_u8p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int]
         L.ecfast_force_isa.argtypes = [ctypes.c_char_p]
+        L.ecfast_encode_batched.restype = ctypes.c_int
+        L.ecfast_encode_batched.argtypes = [_u8p, ctypes.c_int, ctypes.c_int, _u64p, _u32p,
+                                            _u64p, ctypes.c_uint32, ctypes.c_uint32,
+                                            ctypes.c_int]
         _lib = L
     return _lib
 
@@ -222,3 +226,22 @@ def fast_rs_encode(coeff, shards, outs=None, nthreads: int = 1) -> list:
     lib().ecfast_rs_encode(_u8(coeff), k, m, _ptr_array(shards), _ptr_array(outs), n,
                            nthreads)
     return outs
+
+
+def fast_encode_batched(coeff, dptr: np.ndarray, dlen: np.ndarray, pptr: np.ndarray,
+                        unit_bytes: int, nthreads: int = 1) -> None:
+    """ecfast_encode_batched over descriptor arrays of host addresses:
+    dptr / dlen [n_stripes, k] (0 = absent unit), pptr [n_stripes, m]; the
+    caller keeps the memory they point at alive."""
+    coeff = np.ascontiguousarray(coeff, np.uint8)
+    m, k = coeff.shape
+    dptr = np.ascontiguousarray(dptr, np.uint64)
+    dlen = np.ascontiguousarray(dlen, np.uint32)
+    pptr = np.ascontiguousarray(pptr, np.uint64)
+    ns = dptr.shape[0]
+    if dptr.shape != (ns, k) or dlen.shape != (ns, k) or pptr.shape != (ns, m):
+        raise ValueError("descriptor shapes do not match (n_stripes, k) / (n_stripes, m)")
+    if lib().ecfast_encode_batched(_u8(coeff), k, m, dptr.ctypes.data_as(_u64p),
+                                   dlen.ctypes.data_as(_u32p), pptr.ctypes.data_as(_u64p),
+                                   ns, unit_bytes, nthreads) != 0:
+        raise MemoryError("ecfast_encode_batched failed")

@@ -278,3 +278,88 @@ void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
   run_threads(base, n, nthreads);
   free(tabs);
 }
+
+/* ---- batched stripes (configs 4 and 5) -------------------------------- */
+
+typedef struct {
+  const uint64_t* dptr; /* [S][k], 0 = absent */
+  const uint32_t* dlen; /* [S][k] valid bytes */
+  const uint64_t* pptr; /* [S][m] */
+  const coef_tab* tabs;
+  int k, m;
+  uint32_t unit_bytes;
+  uint32_t s_lo, s_hi; /* stripes of this thread */
+} bjob;
+
+/* Stripes [s_lo, s_hi): units with all unit_bytes valid are read in place;
+ * a short or absent unit is copied, zero-padded, into this thread's
+ * k x unit_bytes scratch (the code treats bytes past a unit's length as
+ * zeros, as ecref_encode_batched does). */
+static void* bthread_main(void* arg) {
+  const bjob* B = (const bjob*)arg;
+  const uint32_t U = B->unit_bytes;
+  uint8_t* scratch = NULL;
+  const uint8_t* data[64];
+  uint8_t* par[EC_ORACLE_MAX_M];
+  for (uint32_t s = B->s_lo; s < B->s_hi; ++s) {
+    for (int j = 0; j < B->k; ++j) {
+      const uint8_t* p = (const uint8_t*)(uintptr_t)B->dptr[(uint64_t)s * B->k + j];
+      uint32_t len = p ? B->dlen[(uint64_t)s * B->k + j] : 0;
+      if (len > U) len = U;
+      if (len == U) {
+        data[j] = p;
+        continue;
+      }
+      if (!scratch && !(scratch = (uint8_t*)malloc((size_t)B->k * U))) return (void*)1;
+      uint8_t* pad = scratch + (size_t)j * U;
+      if (len) memcpy(pad, p, len);
+      memset(pad + len, 0, U - len);
+      data[j] = pad;
+    }
+    for (int i = 0; i < B->m; ++i)
+      par[i] = (uint8_t*)(uintptr_t)B->pptr[(uint64_t)s * B->m + i];
+    job J = {data, par, B->tabs, B->k, B->m, 0, U};
+    thread_main(&J);
+  }
+  free(scratch);
+  return NULL;
+}
+
+int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* data_ptrs,
+                          const uint32_t* data_len, const uint64_t* parity_ptrs,
+                          uint32_t n_stripes, uint32_t unit_bytes, int nthreads) {
+  if (k < 1 || k > 64 || m < 1 || m > EC_ORACLE_MAX_M) return -1;
+  if (nthreads < 1) nthreads = 1;
+  if ((uint32_t)nthreads > n_stripes) nthreads = n_stripes ? (int)n_stripes : 1;
+  const size_t bytes = (sizeof(coef_tab) * (size_t)(k * m) + 63) & ~(size_t)63;
+  coef_tab* tabs = (coef_tab*)aligned_alloc(64, bytes);
+  if (!tabs) return -1;
+  for (int i = 0; i < m * k; ++i) make_tab(coeff[i], &tabs[i]);
+  pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+  char* created = (char*)calloc((size_t)nthreads, 1);
+  bjob* jobs = (bjob*)calloc((size_t)nthreads, sizeof(bjob));
+  int status = (th && created && jobs) ? 0 : -1;
+  const uint32_t per = n_stripes / (uint32_t)nthreads, extra = n_stripes % (uint32_t)nthreads;
+  uint32_t s0 = 0;
+  for (int t = 0; status == 0 && t < nthreads; ++t) {
+    const uint32_t cnt = per + ((uint32_t)t < extra ? 1u : 0u);
+    bjob b = {data_ptrs, data_len, parity_ptrs, tabs, k, m, unit_bytes, s0, s0 + cnt};
+    jobs[t] = b;
+    s0 += cnt;
+    /* The calling thread takes the last share itself. */
+    if (t == nthreads - 1 || pthread_create(&th[t], NULL, bthread_main, &jobs[t]) != 0) {
+      if (bthread_main(&jobs[t]) != NULL) status = -1;
+    } else {
+      created[t] = 1;
+    }
+  }
+  for (int t = 0; t < nthreads; ++t) {
+    void* r = NULL;
+    if (created[t] && pthread_join(th[t], &r) == 0 && r != NULL) status = -1;
+  }
+  free(th);
+  free(created);
+  free(jobs);
+  free(tabs);
+  return status;
+}

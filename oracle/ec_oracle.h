@@ -64,6 +64,11 @@ void ecfast_xor_encode(const uint8_t* const* data, int k, uint8_t* parity,
 void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
                       const uint8_t* const* data, uint8_t* const* parity,
                       uint64_t n, int nthreads);
+/* ecref_encode_batched's stripes on nthreads threads (whole stripes per
+ * thread); 0, or -1 for bad arguments or out of memory */
+int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* data_ptrs,
+                          const uint32_t* data_len, const uint64_t* parity_ptrs,
+                          uint32_t n_stripes, uint32_t unit_bytes, int nthreads);
 /* force an ISA ("gfni512", "avx512", "avx2", "scalar"); 0 if unsupported */
 int ecfast_force_isa(const char* name);
 

@@ -35,6 +35,120 @@ def same(a, b):
         for x, y in zip(a, b))
 
 
+def lose_storage(mgr):
+    """This rank's local checkpoint directory is gone (a replaced node)."""
+    shutil.rmtree(mgr.local_dir)
+    os.makedirs(mgr.local_dir)
+
+
+class GroupSpy:
+    """Reports the given process groups as NCCL (as the reference's
+    data-parallel group is, megatron/core/parallel_state.py:730-736) and
+    fails any CPU-tensor collective issued on them: the strategy must run
+    its exchange on a gloo group of its own."""
+
+    def __init__(self, groups):
+        self.groups = [g for g in groups if g is not None]
+        self.orig = {n: getattr(dist, n) for n in
+                     ("get_backend", "all_gather", "all_reduce", "isend", "irecv", "barrier")}
+
+    def __enter__(self):
+        def backend(group=None):
+            if any(group is g for g in self.groups):
+                return "nccl"
+            return self.orig["get_backend"](group)
+
+        def guard(name):
+            fn = self.orig[name]
+
+            def wrapped(*a, **kw):
+                g = kw.get("group")
+                if any(g is x for x in self.groups):
+                    raise AssertionError(f"dist.{name} on the NCCL coding group")
+                return fn(*a, **kw)
+            return wrapped
+
+        dist.get_backend = backend
+        for n in ("all_gather", "all_reduce", "isend", "irecv", "barrier"):
+            setattr(dist, n, guard(n))
+        return self
+
+    def __exit__(self, *exc):
+        for n, fn in self.orig.items():
+            setattr(dist, n, fn)
+
+
+def group_scenario(rank, world, root, scenario, unit, codec_cls, mods):
+    """Coding groups other than the world: the reference's replication test
+    runs cliques of ranks and loses ranks [6, 3, 4]
+    (tests/unit_tests/dist_checkpointing/test_replication.py:75-80,146-160).
+
+    strided  two data-parallel groups [0, 2, 4, 6] and [1, 3, 5, 7] (TP = 2),
+             reported as NCCL: save, lose ranks 6, 3 and 4, load, concurrently
+             in both groups, synchronously and staged in the background;
+    cliques  the coding groups [2, 6, 7], [1, 3], [0, 4, 5] (uneven, not
+             contiguous), each with its gloo twin passed as ``gloo_group``;
+             lose ranks 6, 3 and 4, load."""
+    CheckpointingException, ECLocalCheckpointManager, ErasureCodedStrategy, TensorListState = mods
+    assert world == 8
+    if scenario == "strided":
+        layout = [[0, 2, 4, 6], [1, 3, 5, 7]]
+    else:
+        layout = [[2, 6, 7], [1, 3], [0, 4, 5]]
+    # every rank creates every group, in the same order (as Megatron does)
+    groups = [dist.new_group(g) for g in layout]
+    twins = [dist.new_group(g, backend="gloo") for g in layout] if scenario == "cliques" else None
+    gi = next(i for i, g in enumerate(layout) if rank in g)
+    group, members = groups[gi], layout[gi]
+    G = len(members)
+    k, m = (2, 2) if G == 4 else (G - 1, 1)
+    mine = make_tensors(rank)
+    state = TensorListState([t.clone() for t in mine], {"rank": rank})
+    spy = GroupSpy(groups if scenario == "strided" else [])
+    with spy:
+        if scenario == "strided":
+            strat = ErasureCodedStrategy.from_ec_params(k, m, unit, jump=2, group=group,
+                                                        codec=codec_cls(k, m, unit))
+            assert strat.jump == 1, strat.jump          # global stride 2 = one member
+            comm = strat.comm_group()
+            assert comm is not group
+            assert dist.get_process_group_ranks(comm) == members
+        else:
+            strat = ErasureCodedStrategy(k, m, unit, group=group, codec=codec_cls(k, m, unit),
+                                         gloo_group=twins[gi])
+            assert strat.comm_group() is twins[gi]
+        mgr = ECLocalCheckpointManager(root, strat, stage_in_background=True)
+        mgr.save(state, 1)
+        idx = members.index(rank)
+        names = sorted(f.name for f in mgr.local_dir.iterdir())
+        want = sorted(f"iter_0000001_{members[(idx - p) % G]}_local.ec{p}" for p in range(k + m))
+        assert names == want, (names, want)
+        if scenario == "strided":
+            # a background save in flight, then a foreground find_latest on the
+            # same private group: the foreground waits for it
+            req = mgr.save(state, 2, is_async=True)
+            for t in state.tensors:
+                bump(t)
+            req.execute_sync()
+            assert mgr.find_latest() == 2
+        dist.barrier()   # world-wide, outside the spy's groups: every save is on disk
+        if rank in (6, 3, 4):
+            lose_storage(mgr)
+        dist.barrier()
+        it = mgr.find_latest()
+        assert it == (2 if scenario == "strided" else 1), it
+        got, name = mgr.load()
+        assert name == f"iter_{it:07d}_{rank}_local", name
+        assert same(got.tensors, mine) and got.common == {"rank": rank}
+        if scenario == "strided":
+            # a second manager over the same ranks shares the private group
+            mgr2 = ECLocalCheckpointManager(root + "_b", ErasureCodedStrategy(
+                k, m, unit, group=group, codec=codec_cls(k, m, unit)))
+            mgr2.save(state, 7)
+            got, _ = mgr2.load()
+            assert same(got.tensors, state.tensors)
+
+
 def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1):
     try:
         sys.path.insert(0, ROOT)
@@ -54,6 +168,14 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
         else:
             from ec_cpu_codec import OracleSliceCodec
             codec = OracleSliceCodec(k, m, unit)
+        if scenario in ("strided", "cliques"):
+            from ec_cpu_codec import OracleSliceCodec
+            group_scenario(rank, world, root, scenario, unit, OracleSliceCodec,
+                           (CheckpointingException, ECLocalCheckpointManager,
+                            ErasureCodedStrategy, TensorListState))
+            dist.barrier()
+            dist.destroy_process_group()
+            return
         strat = ErasureCodedStrategy(k, m, unit, codec=codec, jump=jump)
         mgr = ECLocalCheckpointManager(root, strat,
                                        stage_in_background=scenario.startswith("background"))
@@ -76,6 +198,18 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             got, name = mgr.load()
             assert name == f"iter_0000001_{rank}_local", name
             assert same(got.tensors, mine) and got.common == {"rank": rank}
+        elif scenario == "loss_634":
+            # The reference's loss pattern (test_replication.py:146-160): ranks
+            # 6, 3 and 4 of 8 lose their local checkpoint; a code with m = 3
+            # still loads iteration 1 on every rank.
+            mgr.save(state, 1)
+            dist.barrier()
+            if rank in (6, 3, 4):
+                lose_storage(mgr)
+            dist.barrier()
+            assert mgr.find_latest() == 1
+            got, name = mgr.load()
+            assert name == f"iter_0000001_{rank}_local" and same(got.tensors, mine)
         elif scenario in ("node_lost", "node_lost_adjacent"):
             # Two ranks per node, numbered node-major; node 1 (ranks 2, 3) loses
             # its storage.  With jump = 2 every rank's slices sit on distinct

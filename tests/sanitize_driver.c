@@ -124,6 +124,16 @@ int main(void) {
     memcpy(par2, par, sizeof par);
     ecref_encode_batched(coeff, K, M, dp, ln, pp, S, U);
     if (memcmp(par, par2, sizeof par)) FAIL("update != re-encode");
+    /* the SIMD batched encoder on the same grid (short units read only up
+     * to their length, the absent slot as zeros), 1 and 4 threads */
+    for (int th = 1; th <= 4; th += 3) {
+      uint8_t par3[S * M * U];
+      uint64_t pp3[S * M];
+      memset(par3, 0xEE, sizeof par3);
+      for (int q = 0; q < S * M; ++q) pp3[q] = (uint64_t)(uintptr_t)(par3 + (size_t)q * U);
+      if (ecfast_encode_batched(coeff, K, M, dp, ln, pp3, S, U, th) != 0) FAIL("fast batched");
+      if (memcmp(par3, par, sizeof par)) FAIL("fast batched differs (%d threads)", th);
+    }
     for (int q = 0; q < S * K; ++q) free(u[q]);
   }
   printf("sanitize driver ok\n");

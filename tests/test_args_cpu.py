@@ -74,7 +74,9 @@ def test_build_context(tmp_path):
         mgr = ctx["local_checkpoint_manager"]
         assert isinstance(mgr, ECLocalCheckpointManager)
         st = mgr.strategy
-        assert (st.k, st.m, st.unit_bytes, st.jump) == (2, 1, 4096, 3)
+        # --ec-jump is a spacing in global ranks, converted to a spacing of the
+        # coding group's members: over a one-rank world that is one member
+        assert (st.k, st.m, st.unit_bytes, st.jump) == (2, 1, 4096, 1)
         assert mgr.local_dir == tmp_path / "0"
         assert mgr.find_latest() == -1
         assert mgr.stage_in_background   # the default

@@ -75,9 +75,11 @@ def test_gpu_empty_tensor_list(pkg, dev):
     assert codec.decode(meta, {p: slices[p] for p in (1, 2, 4, 5)}, dev) == []
 
 
-def test_gpu_encode_reuses_host_array_only_when_free(pkg, dev):
-    """A live slice keeps its host array out of the next encode; once every
-    slice is dropped the next encode of the same shape writes into it."""
+def test_gpu_encode_reuses_host_array_only_after_release(pkg, dev):
+    """An encode's host array is written again only after the caller hands
+    it back with release(): without that, even with every slice dropped, the
+    next encode takes a fresh array; after it, the next encode of the same
+    shape writes into the released one, with the right bytes."""
     from megatron_lm_amd.checkpoint import GpuSliceCodec
     cpu = make_tensors(3)
     gpu = [t.to(dev) for t in cpu]
@@ -88,14 +90,20 @@ def test_gpu_encode_reuses_host_array_only_when_free(pkg, dev):
     meta2, second = codec.encode(gpu2)
     assert second[0].base is not first[0].base
     assert all(np.array_equal(a, b) for a, b in zip(first, kept)), "live slices were overwritten"
-    base_id = id(second[0].base)  # an id, not a reference: a reference would keep it busy
-    want = [s.copy() for s in second]
-    del first, second
+    raw = first[0].base.ctypes.data   # a consumer that keeps only the address of the first
+    held = first[0].base
+    del first
     meta3, third = codec.encode(gpu2)
-    assert id(third[0].base) == base_id
-    assert meta3 == meta2 and all(np.array_equal(a, b) for a, b in zip(third, want))
+    assert third[0].base.ctypes.data != raw and np.array_equal(held[0], kept[0])
+    want = [s.copy() for s in second]
+    base = second[0].base
+    codec.release(second)
+    del second
+    meta4, fourth = codec.encode(gpu2)
+    assert fourth[0].base is base     # the released array, written again
+    assert meta4 == meta2 and all(np.array_equal(a, b) for a, b in zip(fourth, want))
     _, oracle_slices = OracleSliceCodec(4, 2, 1024).encode([t.cpu() for t in gpu2])
-    assert all(np.array_equal(a, b) for a, b in zip(third, oracle_slices))
+    assert all(np.array_equal(a, b) for a, b in zip(fourth, oracle_slices))
 
 
 @pytest.mark.parametrize("k,m,unit,chunk_stripes", [(4, 2, 1024, None), (6, 3, 4096, 2),

@@ -2,11 +2,12 @@
 RS(6,3) 6 x 256 MiB encode and 3-erasure decode, RS(8,2) over a 20.8 GB rank
 buffer in 4 MiB units, RS(12,4) over 3,000 ragged tensors with a 1% update.
 
-Bit-exact comparisons against the CPU encoder (oracle/ec_cpu_fast.c, itself
-pinned to the scalar oracle by test_oracle.py) where the bytes fit a host
-check in seconds; otherwise size-independent properties over the whole
-buffer (erase -> decode round trips, update == full re-encode) plus
-bit-exact checks of sampled stripes.
+Every output is compared byte for byte against the CPU encoder
+(oracle/ec_cpu_fast.c, itself pinned to the scalar oracle by test_oracle.py)
+on the same seeded numpy bytes: configs 1 and 2 whole, configs 4 and 5 stripe
+by stripe over the whole buffer, the config-3 decode against the original
+shards.  On top, size-independent properties over the whole buffer: erase ->
+decode round trips and update == full re-encode.
 """
 import os
 
@@ -88,36 +89,36 @@ def test_config3_every_erasure_pattern_full_size(pkg, rs63):
     assert n == 129
 
 
-def _check_sampled_stripes(layout, parity, stripes):
-    """Bit-exact check of the given stripes against the CPU encoder on host
-    copies of their zero-padded units."""
+def _check_every_stripe(layout, parity, host_views, what):
+    """Every stripe's parity, byte for byte, against the SIMD CPU encoder
+    (itself pinned to the scalar oracle by test_oracle.py) run over host
+    descriptors of the same bytes, on all usable cores."""
+    from megatron_lm_amd.layout import stripe_descriptors
     k, m, unit = layout.k, layout.m, layout.unit_bytes
-    for s in stripes:
-        units = []
-        for j in range(k):
-            buf = np.zeros(unit, np.uint8)
-            u = s * k + j
-            if u < layout.n_units:
-                v = layout.unit_view(u).cpu().numpy()
-                buf[: v.size] = v
-            units.append(buf)
-        want = oracle.fast_rs_encode(layout.coeff, units, nthreads=THREADS)
-        got = parity[s].cpu().numpy()
-        for i in range(m):
-            assert np.array_equal(got[i], want[i]), f"stripe {s} parity {i}"
+    _, hptr, hlen = stripe_descriptors([v.ctypes.data for v in host_views],
+                                       [v.size for v in host_views], k, unit)
+    assert hptr.shape == (layout.n_stripes, k) and np.array_equal(hlen, layout.host_len)
+    want = np.empty((layout.n_stripes, m, unit), np.uint8)
+    pp = (np.uint64(want.ctypes.data) + np.arange(layout.n_stripes * m, dtype=np.uint64)
+          .reshape(layout.n_stripes, m) * np.uint64(unit))
+    oracle.fast_encode_batched(layout.coeff, hptr, hlen, pp, unit, nthreads=THREADS)
+    got = parity.cpu().numpy()
+    bad = np.flatnonzero((got != want).reshape(layout.n_stripes, -1).any(axis=1))
+    assert bad.size == 0, f"{what}: {bad.size} stripes differ, first {bad[:8].tolist()}"
+    _say(f"{what}: all {layout.n_stripes} stripes byte-identical to the CPU encoder")
 
 
 def test_config4_gpt13b_rank_buffer_rs82(pkg, dev, synth):
-    _say("config 4: 20.8 GB rank buffer, RS(8,2), 4 MiB units")
-    buf = synth.gpt_rank_buffer(dev, seed=4)
+    _say("config 4: 20.8 GB rank buffer, RS(8,2), 4 MiB units (numpy, seeded)")
+    host = synth.gpt_rank_buffer_host(seed=4)
+    buf = torch.from_numpy(host).to(dev)
     pset = pkg.encode([buf], 8, 2, 4 * MiB)
     lay = pset.layout
     assert lay.n_stripes == -(-buf.numel() // (8 * 4 * MiB))
     torch.cuda.synchronize()
+    _check_every_stripe(lay, pset.parity, [host], "config 4")
+    del host
     rng = np.random.default_rng(4)
-    sample = sorted(set(rng.choice(lay.n_stripes, 12, replace=False).tolist()) | {lay.n_stripes - 1})
-    _say(f"config 4: {lay.n_stripes} stripes; checking {len(sample)} against the CPU encoder")
-    _check_sampled_stripes(lay, pset.parity, sample)
     # Round trip over every stripe: lose one data and one parity position.
     lost = [int(rng.integers(0, 8)), 8 + int(rng.integers(0, 2))]
     ref_buf, ref_par = buf.clone(), pset.parity.clone()
@@ -135,21 +136,17 @@ def test_config4_gpt13b_rank_buffer_rs82(pkg, dev, synth):
 
 
 def test_config5_ragged_3000_rs124_and_update(pkg, dev, synth):
-    _say("config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units")
-    sizes, kinds = synth.ragged_sizes(5)
-    tensors = []
-    for i, (n, kind) in enumerate(zip(sizes.tolist(), kinds.tolist())):
-        dt = torch.bfloat16 if kind == 0 else torch.float32
-        t = torch.empty(n // (2 if kind == 0 else 4), dtype=dt, device=dev)
-        synth.device_normal_(t, 5000 + i, 0.02 if kind == 0 else 1e-3, dt)
-        tensors.append(t)
+    _say("config 5: 3,000 ragged tensors, RS(12,4), 64 KiB units (numpy, seeded)")
+    block, views, kinds = synth.ragged_host(5)
+    tensors = [torch.from_numpy(v).to(dev).view(torch.bfloat16 if kd == 0 else torch.float32)
+               for v, kd in zip(views, kinds.tolist())]
     pset = pkg.encode(tensors, 12, 4, 64 << 10)
     lay = pset.layout
     _say(f"config 5: {lay.data_bytes / 1e9:.2f} GB in {lay.n_units} units, {lay.n_stripes} stripes")
-    rng = np.random.default_rng(5)
-    sample = sorted(set(rng.choice(lay.n_stripes, 24, replace=False).tolist()) | {lay.n_stripes - 1})
     torch.cuda.synchronize()
-    _check_sampled_stripes(lay, pset.parity, sample)
+    _check_every_stripe(lay, pset.parity, views, "config 5")
+    del block, views
+    rng = np.random.default_rng(5)
     # Incremental update after a seeded 1% perturbation == full re-encode.
     changed = synth.perturbed_units(5, lay.n_units, 0.01)
     olds = []

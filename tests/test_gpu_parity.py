@@ -594,3 +594,43 @@ def test_stage_to_device(pkg, dev, rows, row_bytes, pitch, pinned, threads):
     for r in range(rows):
         assert np.array_equal(got[r, :row_bytes], host[r]), r
         assert (got[r, row_bytes:] == 0x5A).all(), r
+
+
+@pytest.mark.parametrize("n,offset", [((1 << 20) + 5, 0), (4096 * 3 + 7, 3)])
+def test_shard_plan_matches_oracle(pkg, dev, n, offset):
+    """ShardPlan (a flat call prepared once): RS(6,3) encode, a 3-erasure
+    decode and XOR(4), each launched twice on torch's stream and once on
+    another stream, byte-equal to the oracle; a second launch after the
+    inputs changed codes the new bytes."""
+    rng = np.random.default_rng(n)
+    d = _host(rng, 6, n)
+    dd = _to_dev(d, dev, offset)
+    C = oracle.cauchy(6, 3)
+    enc = pkg.ShardPlan(C, dd)
+    for _ in range(2):
+        par = enc()
+        for p, w in zip(par, oracle.rs_encode(C, d)):
+            assert _eq(p, w)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    for t in par:
+        t.zero_()
+    side.wait_stream(torch.cuda.current_stream(dev))
+    enc(stream=side)
+    side.synchronize()
+    for p, w in zip(par, oracle.rs_encode(C, d)):
+        assert _eq(p, w)
+    lost = [1, 4, 7]
+    surv, rows = pkg.decode_matrix(C, lost)
+    cw = dd + par
+    dec = pkg.ShardPlan(rows, [cw[s] for s in surv], what="ec_rs_decode")
+    for r, g in zip(dec(), lost):
+        assert _eq(r, d[g] if g < 6 else oracle.rs_encode(C, d)[g - 6])
+    xp = pkg.ShardPlan(None, dd[:4], what="ec_xor_encode")
+    assert _eq(xp()[0], oracle.xor_encode(d[:4]))
+    d2 = _host(rng, 6, n)
+    for t, a in zip(dd, d2):
+        t.copy_(torch.from_numpy(a))
+    assert _eq(xp()[0], oracle.xor_encode(d2[:4]))
+    for p, w in zip(enc(), oracle.rs_encode(C, d2)):
+        assert _eq(p, w)

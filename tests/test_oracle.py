@@ -267,6 +267,33 @@ def test_fast_encoder_matches_oracle(isa):
         oracle.fast_force_isa(default)
 
 
+@pytest.mark.parametrize("isa", ["scalar", "avx2", "avx512", "gfni512"])
+def test_fast_batched_encoder_matches_oracle(isa):
+    """The SIMD batched encoder (the CPU baseline and full-size checker of
+    configs 4 and 5) equals the scalar oracle's batched encode on ragged
+    stripes with short and absent units, for several thread counts."""
+    default = oracle.fast_isa()
+    if not oracle.fast_force_isa(isa):
+        pytest.skip(f"{isa} not supported on this host")
+    try:
+        rng = np.random.default_rng(22)
+        for k, m, unit, threads in [(12, 4, 96, 3), (8, 2, 4096, 2), (6, 3, 64, 1),
+                                    (4, 1, 1024, 7)]:
+            grid, glen = _ragged(rng, k, unit)
+            C = oracle.cauchy(k, m)
+            want = oracle.encode_batched(C, grid, glen, unit)
+            ns = len(grid)
+            dptr = np.array([[0 if u is None else u.ctypes.data for u in row] for row in grid],
+                            np.uint64).reshape(ns, k)
+            got = np.full((ns, m, unit), 0xEE, np.uint8)
+            pptr = np.array([[got[s, i].ctypes.data for i in range(m)] for s in range(ns)],
+                            np.uint64).reshape(ns, m)
+            oracle.fast_encode_batched(C, dptr, glen, pptr, unit, nthreads=threads)
+            assert np.array_equal(got, want), (k, m, unit, threads)
+    finally:
+        oracle.fast_force_isa(default)
+
+
 # ------------------------------------------------------------------ golden --
 
 def _golden(name):

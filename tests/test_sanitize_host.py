@@ -1,7 +1,9 @@
-"""Host code under AddressSanitizer and UndefinedBehaviorSanitizer: the C
-oracle, the SIMD CPU encoder and the engine's host GF(2^8) code
-(megatron-lm_amd/csrc/gf256.cpp), built with gcc/g++ on their own (no device
-code) and driven by tests/sanitize_driver.c."""
+"""Host code under AddressSanitizer and UndefinedBehaviorSanitizer, built with
+gcc/g++ on their own (no device code): the C oracle, the SIMD CPU encoder
+(flat and batched) and the engine's host GF(2^8) code
+(megatron-lm_amd/csrc/gf256.cpp), driven by tests/sanitize_driver.c; and the
+staging entry points' multi-threaded host copies
+(megatron-lm_amd/csrc/host_copy.cpp), driven by tests/sanitize_copy_driver.cpp."""
 import os
 import subprocess
 
@@ -27,3 +29,17 @@ def test_host_code_is_sanitizer_clean(tmp_path):
     out = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=300)
     assert out.returncode == 0, out.stderr[-4000:]
     assert "sanitize driver ok" in out.stdout
+
+
+def test_staging_host_copies_are_sanitizer_clean(tmp_path):
+    csrc = os.path.join(ROOT, "megatron-lm_amd", "csrc")
+    exe = str(tmp_path / "copydrv")
+    subprocess.run(["g++", "-std=c++17", *SAN, "-I", csrc,
+                    os.path.join(csrc, "host_copy.cpp"),
+                    os.path.join(ROOT, "tests", "sanitize_copy_driver.cpp"),
+                    "-o", exe, "-pthread"], check=True)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="print_stacktrace=1")
+    env.pop("LD_PRELOAD", None)
+    out = subprocess.run([exe], capture_output=True, text=True, env=env, timeout=300)
+    assert out.returncode == 0, out.stderr[-4000:]
+    assert "sanitize copy driver ok" in out.stdout
