@@ -12,6 +12,20 @@ namespace {
 // Grid = n_stripes x tiles_per_unit workgroups, stripe-major, so consecutive
 // workgroups stream adjacent bytes of the same k units.  The descriptor of a
 // stripe is uniform across the workgroup (scalar loads).
+//
+// The product launches one-wavefront workgroups with one 16-byte chunk per
+// lane, one 1 KiB tile of one stripe per workgroup (kBatchBlock, U = 1).
+// Measured on MI355X (HBM traffic, GB/s) against the former launcher
+// (256-lane workgroups walking 8-16 KiB of a stripe; four chunks per lane for
+// k <= 8 and units that are a multiple of 16 KiB): config 5's RS(12,4) over
+// 3,000 ragged tensors in 64 KiB units, encode 6271 -> 6316, copying encode
+// 5440 -> 5791, decode of 4 positions 5559 -> 6124; RS(12,4) over 4 MiB
+// units encode 5417 -> 5681, decode 5195 -> 5926; RS(6,3) over 1 MiB units
+// encode 5999 -> 6651, decode 5844 -> 6424; RS(8,2) over 64 KiB units
+// copying encode 5493 -> 6060, decode 6010 -> 6162, encode 6712 -> 6497; the
+// 20.8 GB config 4 (RS(8,2), 4 MiB units) encode 5800 -> 5767.  Spans of
+// 4 KiB per workgroup or 128-lane workgroups were in between.
+constexpr int kBatchBlock = 64;
 
 template <int K, int M>
 struct BatchArgs {
@@ -23,16 +37,16 @@ struct BatchArgs {
                          // unit_bytes (0 = no copy); read only when the kernel copies
   PermTab tab[M][K];
   uint32_t unit_bytes;
-  uint32_t tiles_per_unit;   // tiles of kBlock*U*16 bytes in a unit
+  uint32_t tiles_per_unit;   // tiles of B*U*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
 };
 
-// 16 KiB of zeros in device memory, read-only: on the fast path a unit that
-// ended before the current tile is read from here instead of branching, so
-// the tile's k loads stay unconditional.  (Covers a tile of kBlock * U * 16
-// bytes for U <= 4.)
-__device__ __align__(16) uint8_t g_zero_tile[kBlock * 4 * 16] = {0};
+// Zeros in device memory, read-only: on the fast path a unit that ended
+// before the current tile is read from here instead of branching, so the
+// tile's k loads stay unconditional.  (Covers a tile of B * U * 16 bytes for
+// B * U <= 1024.)
+__device__ __align__(16) uint8_t g_zero_tile[1024 * 16] = {0};
 
 // One tile of a stripe in which no unit ends strictly inside the tile and
 // every output covers it (almost every tile).  src[j] points at the tile's
@@ -44,21 +58,21 @@ __device__ __align__(16) uint8_t g_zero_tile[kBlock * 4 * 16] = {0};
 // With COPY, cpy[j] points at the tile's first byte of unit j's copy (null:
 // no copy) and the loaded chunk is stored there too: the data is read once
 // for both the parity and the copy.
-template <int K, int M, int U, bool COPY>
+template <int K, int M, int U, bool COPY, int B>
 __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
                                           uint8_t* const (&cpy)[K],
                                           const PermTab (&tab)[M][K]) {
-  static_assert(kBlock * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
+  static_assert(B * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
   uint4 x[U][K];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t rel = (u * kBlock + threadIdx.x) * 16u;
+    const uint32_t rel = (u * B + threadIdx.x) * 16u;
 #pragma unroll
     for (int j = 0; j < K; ++j) x[u][j] = load_stream(src[j] + rel);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t rel = (u * kBlock + threadIdx.x) * 16u;
+    const uint32_t rel = (u * B + threadIdx.x) * 16u;
     uint32_t acc[M][4] = {};
     gf_matvec16<K, M>(acc, x[u], tab);
 #pragma unroll
@@ -76,7 +90,7 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
 // views into a flat buffer at arbitrary offsets): one chunk per lane at a
 // time, each unit read through load_realign (two aligned loads and a byte
 // shift for a misaligned unit); the outputs are aligned.
-template <int K, int M, int U, bool COPY>
+template <int K, int M, int U, bool COPY, int B>
 __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K],
                                                   uint8_t* const (&dst)[M],
                                                   uint8_t* const (&cpy)[K],
@@ -87,13 +101,13 @@ __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K]
     uint4 x[V][K];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+      const uint32_t rel = ((u0 + v) * B + threadIdx.x) * 16u;
 #pragma unroll
       for (int j = 0; j < K; ++j) x[v][j] = load_realign(src[j], rel);
     }
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      const uint32_t rel = ((u0 + v) * kBlock + threadIdx.x) * 16u;
+      const uint32_t rel = ((u0 + v) * B + threadIdx.x) * 16u;
       uint32_t acc[M][4] = {};
       gf_matvec16<K, M>(acc, x[v], tab);
 #pragma unroll
@@ -115,11 +129,11 @@ __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K]
 //
 // With COPY, each unit's chunk (zeros past its valid length) also goes to
 // its copy, over the whole unit_bytes.
-template <int K, int M, int U, bool COPY>
+template <int K, int M, int U, bool COPY, int B>
 __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, uint32_t base,
                                           const PermTab (&tab)[M][K]) {
   for (int u = 0; u < U; ++u) {
-    const uint32_t off = (base + u * kBlock) * 16u;
+    const uint32_t off = (base + u * B) * 16u;
     if (off >= a.unit_bytes) continue;
     uint32_t acc[M][4] = {};
 #pragma unroll 1
@@ -156,8 +170,8 @@ __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, 
   }
 }
 
-template <int K, int M, int U, bool COPY>
-__global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a) {
+template <int K, int M, int U, bool COPY, int B>
+__global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
   // Workgroup b covers tiles [t0, t1) of one stripe: the descriptor loads and
@@ -192,9 +206,9 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
     c[j] = COPY ? reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]) : nullptr;
     out_aligned &= (reinterpret_cast<uintptr_t>(c[j]) & 15u) == 0;
   }
-  constexpr uint32_t kTileBytes = kBlock * U * 16u;
+  constexpr uint32_t kTileBytes = B * U * 16u;
   for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t base = t * (kBlock * U) + threadIdx.x;
+    const uint32_t base = t * (B * U) + threadIdx.x;
     const uint32_t lo = t * kTileBytes, hi = lo + kTileBytes;
     // A tile is an edge tile when some unit ends strictly inside it or some
     // output does not cover it.
@@ -215,15 +229,15 @@ __global__ void __launch_bounds__(kBlock) batched_kernel(const BatchArgs<K, M> a
       edge |= olen[i] < hi;
     }
     if (edge)
-      tile_edge<K, M, U, COPY>(a, s, base, tab);
+      tile_edge<K, M, U, COPY, B>(a, s, base, tab);
     else if (in_aligned)
-      tile_full<K, M, U, COPY>(src, dst, cpy, tab);
+      tile_full<K, M, U, COPY, B>(src, dst, cpy, tab);
     else
-      tile_full_realign<K, M, U, COPY>(src, dst, cpy, tab);
+      tile_full_realign<K, M, U, COPY, B>(src, dst, cpy, tab);
   }
 }
 
-template <int K, int M, int U, bool COPY>
+template <int K, int M, int U, bool COPY, int B>
 int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
                      const uint64_t* pptr, const uint32_t* olen, const uint64_t* cptr,
                      uint32_t n_stripes, uint32_t unit_bytes, hipStream_t st) {
@@ -237,20 +251,18 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
-  a.tiles_per_unit = (unit16 + kBlock * U - 1) / (kBlock * U);
-  // A workgroup walks up to span_bytes() of each unit (at least one tile),
-  // keeping at least 2048 workgroups (8 per CU) in the launch.
-  const uint32_t tile_bytes = kBlock * U * 16u;
-  uint64_t tpb = span_bytes(unit_bytes) / tile_bytes;
+  a.tiles_per_unit = (unit16 + B * U - 1) / (B * U);
+  // One tile per workgroup; spans of consecutive tiles only to keep the grid
+  // below 2^30 workgroups.
   const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
-  if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
+  uint64_t tpb = (total_tiles + 0x3fffffffull) >> 30;
   if (tpb < 1) tpb = 1;
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
-  hipLaunchKernelGGL((batched_kernel<K, M, U, COPY>), dim3((unsigned)blocks), dim3(kBlock), 0,
+  hipLaunchKernelGGL((batched_kernel<K, M, U, COPY, B>), dim3((unsigned)blocks), dim3(B), 0,
                      st, a);
   return hip_status();
 }

@@ -13,20 +13,16 @@
 namespace ec {
 namespace {
 
-// The tile must not be larger than the units, or every tile holds a unit's
-// end and takes the edge path: four chunks per lane (16 KiB tiles) only when
-// the units are a multiple of 16 KiB, else one (4 KiB tiles).  RS(8,2) over
-// 4 KiB units ran at 1.7 TB/s with 16 KiB tiles.
+// One-wavefront workgroups, one 1 KiB tile each (see kBatchBlock).  The tile
+// is also no larger than the smallest units that stream at HBM rate: with
+// 16 KiB tiles every tile of a 4 KiB unit held the unit's end and took the
+// edge path (RS(8,2) over 4 KiB units 1.7 TB/s).
 template <int K, int M>
 int launch_batched(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
                    const uint64_t* pptr, const uint32_t* olen, uint32_t n_stripes,
                    uint32_t unit_bytes, hipStream_t st) {
-  constexpr int U = batched_unroll<K>();
-  if (U > 1 && unit_bytes % (kBlock * U * 16u) == 0)
-    return launch_batched_u<K, M, U, false>(coeff, dptr, dlen, pptr, olen, nullptr, n_stripes,
-                                            unit_bytes, st);
-  return launch_batched_u<K, M, 1, false>(coeff, dptr, dlen, pptr, olen, nullptr, n_stripes,
-                                          unit_bytes, st);
+  return launch_batched_u<K, M, 1, false, kBatchBlock>(coeff, dptr, dlen, pptr, olen, nullptr,
+                                                       n_stripes, unit_bytes, st);
 }
 
 using BatchFn = int (*)(const uint8_t*, const uint64_t*, const uint32_t*, const uint64_t*,

@@ -16,12 +16,8 @@ template <int K, int M>
 int launch_batched_copy(const uint8_t* coeff, const uint64_t* dptr, const uint32_t* dlen,
                         const uint64_t* pptr, const uint64_t* cptr, uint32_t n_stripes,
                         uint32_t unit_bytes, hipStream_t st) {
-  constexpr int U = batched_unroll<K>();
-  if (U > 1 && unit_bytes % (kBlock * U * 16u) == 0)
-    return launch_batched_u<K, M, U, true>(coeff, dptr, dlen, pptr, nullptr, cptr, n_stripes,
-                                           unit_bytes, st);
-  return launch_batched_u<K, M, 1, true>(coeff, dptr, dlen, pptr, nullptr, cptr, n_stripes,
-                                         unit_bytes, st);
+  return launch_batched_u<K, M, 1, true, kBatchBlock>(coeff, dptr, dlen, pptr, nullptr, cptr,
+                                                      n_stripes, unit_bytes, st);
 }
 
 using BatchCopyFn = int (*)(const uint8_t*, const uint64_t*, const uint32_t*, const uint64_t*,

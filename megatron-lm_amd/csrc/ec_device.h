@@ -6,22 +6,23 @@
 // VALU code laid out for streaming.
 //
 // Data layout and mapping.
-//   A shard is a flat byte range.  Lane l of a 256-lane workgroup owns 16
-//   bytes (one global_load_dwordx4) of every shard at chunk index
-//   base + u*256 + l, u < U, so each wavefront reads 1 KiB contiguous per
-//   shard per load and the k loads of a lane are all in flight together.
-//   The m parity outputs of those bytes are accumulated in VGPRs and written
-//   once: every input byte is read from HBM exactly once and every parity
-//   byte written exactly once.  Loads and stores are non-temporal (streamed
-//   past L2 and the Infinity Cache), and for shards below 512 MiB tiles are
-//   renumbered so that the shards are streamed at two places at once
-//   (tile_order).  Measured on
-//   MI355X for RS(6,3) over 256 MiB shards: plain loads/stores and tables in
-//   SGPRs 5.48 TB/s of HBM traffic; streaming access 5.90; plus LDS tables
-//   6.15; the two-place order with one chunk per lane 6.29-6.54 over five
-//   buffer layouts, where one window per XCD gave 5.69-6.22 (see
-//   gf_matvec16 for the table-read order that keeps wider codes at the same
-//   rate).
+//   A shard is a flat byte range.  Lane l of a workgroup owns 16 bytes (one
+//   global_load_dwordx4) of every shard at chunk index base + l, so each
+//   wavefront reads 1 KiB contiguous per shard per load and the k loads of a
+//   lane are all in flight together.  The m parity outputs of those bytes are
+//   accumulated in VGPRs and written once: every input byte is read from HBM
+//   exactly once and every parity byte written exactly once.  Loads and
+//   stores are non-temporal (streamed past L2 and the Infinity Cache).  The
+//   flat kernels run 64- or 128-lane workgroups in launch order
+//   (flat_block in ec_flat.hip); the kernels with k at run time and the
+//   batched ones 256-lane workgroups.  Measured on MI355X for RS(6,3) over
+//   256 MiB shards (HBM traffic): plain loads/stores and tables in SGPRs
+//   5.48 TB/s; streaming access 5.90; plus LDS tables 6.15; 256-lane
+//   workgroups streaming each shard at two places (even XCDs the first
+//   half, odd XCDs the second) 5.9-6.5 depending on
+//   the box and the buffer layout; one-wavefront workgroups in launch order
+//   6.4 (see gf_matvec16 for the table-read order that keeps wider codes at
+//   the same rate).
 //
 // GF multiply by a coefficient c (see PermTab in gf256.h): the byte x is cut
 // into fields x[2:0], x[5:3], x[7:6]; each field indexes an 8- or 4-entry
@@ -56,14 +57,12 @@ namespace {
 constexpr int kBlock = 256;     // lanes per workgroup (4 wavefronts)
 constexpr int kFastMaxK = 16;   // template-instantiated shard counts
 constexpr int kFastMaxM = 4;
-// Bytes of each unit a batched workgroup walks: 8 KiB for units up to
-// 256 KiB, 16 KiB above, and never less than one tile.  Measured on MI355X
-// (HBM traffic, two chunks per lane for k <= 8), spans of 64/32/16/8 KiB:
-// RS(8,2) over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2) over 64 KiB
-// units 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units
-// 5.87/5.86/6.13/6.22.  With four chunks per lane (batched_unroll, units
-// that are a multiple of 16 KiB) a k <= 8 tile is 16 KiB, so those codes run
-// one tile per workgroup.
+// Bytes of each unit a workgroup of the batched kernels for wide codes
+// (batched_wide_kernel, 4 KiB tiles) walks: 8 KiB for units up to 256 KiB,
+// 16 KiB above.  Measured on MI355X for the fixed-size batched kernel when it
+// ran 256-lane workgroups (HBM traffic), spans of 64/32/16/8 KiB: RS(8,2)
+// over 4 MiB units 5.31/5.50/5.71/5.54 TB/s; RS(8,2) over 64 KiB units
+// 6.17/6.14/6.32/6.63; RS(12,4) over ragged 64 KiB units 5.87/5.86/6.13/6.22.
 inline uint32_t span_bytes(uint32_t unit_bytes) {
   return unit_bytes <= (256u << 10) ? (8u << 10) : (16u << 10);
 }
@@ -127,30 +126,6 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
 __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
   const u32x4 w = {v.x, v.y, v.z, v.w};
   __builtin_nontemporal_store(w, (global_u32x4*)(uintptr_t)p);
-}
-
-// Two-window tile order.  Workgroups are dispatched round-robin over the 8
-// XCDs (workgroup b runs on XCD b % 8).  Renumbering b -> (b % 2) * per + b / 2
-// gives the even XCDs the first half of the tile range and the odd XCDs the
-// second half, so every shard is streamed at two places half a shard apart.
-// On MI355X, for shards below kSplitMaxBytes, this beat launch order (one
-// place) and one window per XCD (eight places) for every code measured, on
-// every buffer layout tried: separate allocations, one packed block, random
-// 4 KiB offsets, 1 MiB and 12 KiB padding.  From 512 MiB shards on it lost
-// 8-20 % to launch order (RS(6,3): 512 MiB 4.80 vs 5.65 TB/s, 1 GiB 4.93 vs
-// 5.92, 2 GiB 5.06 vs 5.73; up to 448 MiB it won or tied), also with the
-// halves interleaved in segments of 16-256 MiB, so larger shards keep
-// launch order.  A bijection on [0, gridDim.x); an odd last tile keeps its
-// index.
-constexpr uint64_t kSplitMaxBytes = 512ull << 20;
-
-__device__ __forceinline__ uint32_t split_tile(uint32_t b, uint32_t nb) {
-  const uint32_t per = nb >> 1;
-  return b < (per << 1) ? (b & 1u) * per + (b >> 1) : b;
-}
-
-__device__ __forceinline__ uint32_t tile_order(uint32_t b, uint32_t nb, uint64_t n16) {
-  return n16 * 16 < kSplitMaxBytes ? split_tile(b, nb) : b;
 }
 
 // Copy the m x k permute tables from the kernel arguments into LDS, where
@@ -267,8 +242,8 @@ __device__ inline PermTab dev_perm_tab(uint32_t c) {
 
 // ------------------------------------------------------- wide-code knobs --
 // Codes past the instantiated fast path (k > 16 or m > 4, up to 32 x 16) on
-// 16-byte-aligned shards: rs_kernel's column layout and tile order with the
-// m outputs in registers (M is a template parameter) and k read at run time
+// 16-byte-aligned shards: rs_kernel's column layout and launch order with
+// the m outputs in registers (M is a template parameter) and k read at run time
 // in groups of kWideGroup loads in flight.  The m x k tables do not fit the
 // kernel arguments (10 KiB for 16 x 32), so each workgroup builds them in LDS
 // from the coefficient bytes.  Measured over 256 MiB shards (HBM TB/s): a
@@ -360,31 +335,24 @@ __device__ __forceinline__ void store_unit_len(uint8_t* p, uint32_t off, uint32_
 
 inline int hip_status() { return hipGetLastError() == hipSuccess ? EC_OK : EC_EHIP; }
 
-// Grid for a grid-stride kernel over n16 chunks with U chunks per lane:
-// enough workgroups to cover the range once, capped so a launch stays a few
-// waves deep on 256 CUs.
+// Grid for a grid-stride kernel over n16 chunks with U chunks per lane of a
+// kBlock-lane workgroup: enough workgroups to cover the range once, capped so
+// a launch stays a few waves deep on 256 CUs.
 inline unsigned grid_for(uint64_t n16, int U) {
   const uint64_t tiles = (n16 + (uint64_t)kBlock * U - 1) / ((uint64_t)kBlock * U);
   const uint64_t cap = 1u << 20;
   return (unsigned)(tiles < cap ? (tiles ? tiles : 1) : cap);
 }
 
-template <int K>
-constexpr int unroll_for() {
-  return K <= 8 ? 2 : 1;
+// Grid of a grid-stride kernel with `lanes` lanes per workgroup and one chunk
+// per lane: one workgroup per `lanes` chunks, up to 2^24 workgroups (shards
+// up to 16 GiB with 64 lanes are covered in one pass).
+inline unsigned grid_of(uint64_t n16, int lanes) {
+  const uint64_t g = (n16 + (uint64_t)lanes - 1) / (uint64_t)lanes;
+  const uint64_t cap = 1u << 24;
+  return (unsigned)(g < cap ? (g ? g : 1) : cap);
 }
 
-// Chunks per lane of the batched launcher.  For k <= 8 a workgroup takes one
-// 16 KiB tile per unit (U = 4, 222 VGPRs for RS(8,2), two waves per SIMD):
-// fewer workgroups in flight means fewer stripes open at once, and this
-// beat U = 2 with 16 KiB spans by 0-4 % (RS(8,2) over the 20.8 GB rank
-// buffer in 4 MiB units 5.73 -> 5.86 TB/s of traffic; 1 MiB units 5.96 ->
-// 6.19; RS(6,3) in 4 MiB units 5.81 -> 5.96; 64 KiB units 6.52 -> 6.67).
-// Wider codes keep U = 1 (RS(12,4) ragged: U = 2 was 3 % slower).
-template <int K>
-constexpr int batched_unroll() {
-  return K <= 8 ? 4 : 1;
-}
 
 
 inline bool fast_shape(int k, int m) { return k <= kFastMaxK && m <= kFastMaxM; }

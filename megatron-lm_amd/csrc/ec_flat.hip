@@ -28,37 +28,45 @@ struct RsArgs {
   uint64_t n16;
 };
 
-template <int K, int M, int U>
-__global__ void __launch_bounds__(kBlock) rs_kernel(const RsArgs<K, M> a) {
+// Lanes per workgroup of the flat kernels: one wavefront for the small codes
+// (tables in registers, k * m <= 20), two for the wider ones, with
+// workgroups in launch order: workgroup b streams 1 or 2 KiB of every shard
+// at column b * BLOCK, and the round-robin dispatch over the 8 XCDs deals
+// consecutive 1-2 KiB columns to different XCDs.  Measured on MI355X over
+// 256 MiB shards (HBM traffic, GB/s; the former 256-lane workgroups that
+// streamed each shard at two places half a shard apart first): RS(6,3) 5887 -> 6404 (one wave),
+// 6309 (two waves); RS(8,2) 5900 -> 6319 / 6381; RS(4,1) 5942 -> 6347 /
+// 6377; RS(12,4) 5687 -> 6087 / 6253; RS(16,4) over 128 MiB 6116 -> 6291 /
+// 6335.  RS(6,3) with one wave over 64 MiB to 1 GiB shards: 6393-6547
+// (5657-6097 before).  Smaller workgroups also made the rate less dependent
+// on the box: the 256-lane kernel ran RS(6,3) at 393 to 424 us per launch on
+// three boxes, the 64/128-lane ones at 376 to 386.  The two-window order lost
+// with them (RS(6,3) one wave: 6202 vs 6404 at 256 MiB).
+template <int K, int M>
+constexpr int flat_block() {
+  return K * M <= 20 ? 64 : 128;
+}
+
+template <int K, int M>
+__global__ void __launch_bounds__((flat_block<K, M>())) rs_kernel(const RsArgs<K, M> a) {
+  constexpr int B = flat_block<K, M>();
   __shared__ PermTab tab[M][K];
-  stage_tables<K, M>(tab, a.tab);
-  const uint64_t tile = (uint64_t)kBlock * U;
-  const uint64_t stride = (uint64_t)gridDim.x * tile;
-  for (uint64_t base = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * tile + threadIdx.x;
-       base < a.n16; base += stride) {
-    uint4 x[U][K];
+  {
+    // M * K <= 64 tables: one per lane of the first B lanes, looped for
+    // B = 64 < M * K
+    for (int q = threadIdx.x; q < M * K; q += B) tab[q / K][q % K] = a.tab[q / K][q % K];
+    __syncthreads();
+  }
+  const uint64_t stride = (uint64_t)gridDim.x * B;
+  for (uint64_t idx = (uint64_t)blockIdx.x * B + threadIdx.x; idx < a.n16; idx += stride) {
+    uint4 x[K];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint64_t idx = base + (uint64_t)u * kBlock;
-      if (idx < a.n16) {
+    for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + idx * 16);
+    uint32_t acc[M][4] = {};
+    gf_matvec16<K, M>(acc, x, tab);
 #pragma unroll
-        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
-      } else {
-#pragma unroll
-        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint64_t idx = base + (uint64_t)u * kBlock;
-      uint32_t acc[M][4] = {};
-      gf_matvec16<K, M>(acc, x[u], tab);
-      if (idx < a.n16) {
-#pragma unroll
-        for (int i = 0; i < M; ++i)
-          store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
-      }
-    }
+    for (int i = 0; i < M; ++i)
+      store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
   }
 }
 
@@ -76,47 +84,30 @@ __device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uin
                     xor3(a.w, b.w, c.w));
 }
 
-// XOR parity: 512-lane workgroups in launch order (measured on MI355X for
-// XOR(4) over 64 MiB shards: 6.37 TB/s of HBM traffic; 6.21 with 256 lanes;
-// 5.68 with one tile window per XCD and 6.00 with split_tile's two, which
-// only pay off for the RS kernel).
-constexpr int kXorBlock = 512;
+// XOR parity: one-wavefront workgroups in launch order, one chunk per lane.
+// Measured on MI355X for XOR(4) (HBM traffic, GB/s): over 64 MiB shards 6482
+// vs 6357 for the former 512-lane workgroups with two chunks per lane (6399
+// with 128 lanes, 6288 with 256); over 256 MiB 6621 vs 6555.
+constexpr int kXorBlock = 64;
 
-template <int K, int U>
+template <int K>
 __global__ void __launch_bounds__(kXorBlock) xor_kernel(const XorArgs<K> a) {
-  const uint64_t tile = (uint64_t)kXorBlock * U;
-  const uint64_t stride = (uint64_t)gridDim.x * tile;
-  for (uint64_t base = (uint64_t)blockIdx.x * tile + threadIdx.x; base < a.n16;
-       base += stride) {
-    uint4 x[U][K];
+  const uint64_t stride = (uint64_t)gridDim.x * kXorBlock;
+  for (uint64_t idx = (uint64_t)blockIdx.x * kXorBlock + threadIdx.x; idx < a.n16;
+       idx += stride) {
+    uint4 x[K];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint64_t idx = base + (uint64_t)u * kXorBlock;
-      if (idx < a.n16) {
+    for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + idx * 16);
+    uint4 acc = x[0];
+    int j = 1;
 #pragma unroll
-        for (int j = 0; j < K; ++j) x[u][j] = load_stream(a.data[j] + idx * 16);
-      } else {
-#pragma unroll
-        for (int j = 0; j < K; ++j) x[u][j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint64_t idx = base + (uint64_t)u * kXorBlock;
-      uint4 acc = x[u][0];
-      int j = 1;
-#pragma unroll
-      for (; j + 1 < K; j += 2) acc = xor3v(acc, x[u][j], x[u][j + 1]);
-      if (j < K)
-        acc = make_uint4(acc.x ^ x[u][j].x, acc.y ^ x[u][j].y, acc.z ^ x[u][j].z,
-                         acc.w ^ x[u][j].w);
-      if (idx < a.n16) {
-        if (K == 1)  // a plain copy: streaming stores measured 3 % faster
-          store_stream(a.out + idx * 16, acc);
-        else
-          reinterpret_cast<uint4*>(a.out)[idx] = acc;
-      }
-    }
+    for (; j + 1 < K; j += 2) acc = xor3v(acc, x[j], x[j + 1]);
+    if (j < K)
+      acc = make_uint4(acc.x ^ x[j].x, acc.y ^ x[j].y, acc.z ^ x[j].z, acc.w ^ x[j].w);
+    if (K == 1)  // a plain copy: streaming stores measured 3 % faster
+      store_stream(a.out + idx * 16, acc);
+    else
+      reinterpret_cast<uint4*>(a.out)[idx] = acc;
   }
 }
 
@@ -166,14 +157,21 @@ struct WideArgs {
   int k;
 };
 
+// 128-lane workgroups in launch order.  Measured on MI355X (HBM traffic,
+// GB/s; the former 256-lane workgroups that streamed each shard at two
+// places half a shard apart first): RS(20,4) over 256 MiB 5157 -> 5464, RS(24,4) 5124 ->
+// 5385, RS(10,6) over 128 MiB 5280 -> 5311, RS(6,8) 4844 -> 4902, RS(32,16)
+// over 64 MiB 2720 -> 2700 (VALU-bound there).
+constexpr int kWideBlock = 128;
+
 template <int M>
-__global__ void __launch_bounds__(kBlock) wide_kernel(const WideArgs a) {
+__global__ void __launch_bounds__(kWideBlock) wide_kernel(const WideArgs a) {
   __shared__ PermTab tab[M * EC_MAX_K];
   const int k = a.k;
-  for (int t = threadIdx.x; t < M * k; t += kBlock) tab[t] = dev_perm_tab(a.coeff[t]);
+  for (int t = threadIdx.x; t < M * k; t += kWideBlock) tab[t] = dev_perm_tab(a.coeff[t]);
   __syncthreads();
-  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)tile_order(blockIdx.x, gridDim.x, a.n16) * kBlock + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * kWideBlock;
+  for (uint64_t idx = (uint64_t)blockIdx.x * kWideBlock + threadIdx.x;
        idx < a.n16; idx += stride) {
     uint32_t acc[M][4] = {};
     for (int j0 = 0; j0 < k; j0 += kWideGroup) {
@@ -234,10 +232,8 @@ int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, 
   for (int i = 0; i < M; ++i)
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   a.n16 = n16;
-  // One 16-byte chunk per lane per shard: with the two-window order this beat
-  // two chunks by 2-6 % for k <= 8 (k > 8 needs U = 1 for registers anyway).
-  constexpr int U = 1;
-  hipLaunchKernelGGL((rs_kernel<K, M, U>), dim3(grid_for(n16, U)), dim3(kBlock), 0, st, a);
+  constexpr int B = flat_block<K, M>();
+  hipLaunchKernelGGL((rs_kernel<K, M>), dim3(grid_of(n16, B)), dim3(B), 0, st, a);
   return hip_status();
 }
 
@@ -250,7 +246,7 @@ int launch_wide(const uint8_t* coeff, int k, const uint8_t* const* d, uint8_t* c
   for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
   a.n16 = n16;
   a.k = k;
-  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid_for(n16, 1)), dim3(kBlock), 0, st, a);
+  hipLaunchKernelGGL((wide_kernel<M>), dim3(grid_of(n16, kWideBlock)), dim3(kWideBlock), 0, st, a);
   return hip_status();
 }
 
@@ -260,9 +256,7 @@ int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st
   for (int j = 0; j < K; ++j) a.data[j] = d[j];
   a.out = o;
   a.n16 = n16;
-  constexpr int U = unroll_for<K>();
-  hipLaunchKernelGGL((xor_kernel<K, U>), dim3(grid_for(n16, U * (kXorBlock / kBlock))),
-                     dim3(kXorBlock), 0, st, a);
+  hipLaunchKernelGGL((xor_kernel<K>), dim3(grid_of(n16, kXorBlock)), dim3(kXorBlock), 0, st, a);
   return hip_status();
 }
 

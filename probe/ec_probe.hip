@@ -4,10 +4,10 @@
 // against.  Not part of the C ABI of ec_mi355.h and not used by the product
 // path.
 //
-// probe_kernel<R, W> is rs_kernel's memory skeleton: 256-lane workgroups, one
-// 16-byte non-temporal load per lane from each of R streams at the same
-// column, the same two-window tile order, and one non-temporal store to each
-// of W streams; the GF(2^8) arithmetic is replaced by one XOR.  With W = 0
+// probe_kernel<R, W> is the memory skeleton of RS(6,3)'s rs_kernel: one-wave
+// (64-lane) workgroups in launch order, one 16-byte non-temporal load per
+// lane from each of R streams at the same column, and one non-temporal store
+// to each of W streams; the GF(2^8) arithmetic is replaced by one XOR.  With W = 0
 // the XOR result is stored to a 16-byte sink only if all four words equal a
 // value no data hits in practice, which keeps the loads alive; the sink is a
 // valid buffer either way.
@@ -16,7 +16,7 @@
 
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 64;
 constexpr int kMaxStreams = 8;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -29,13 +29,6 @@ __device__ __forceinline__ void store_nt(uint8_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, (global_u32x4*)(uintptr_t)p);
 }
 
-// Same renumbering as the RS kernel: even XCDs take the first half of the
-// tiles, odd XCDs the second half.
-__device__ __forceinline__ uint32_t split_tile(uint32_t b, uint32_t nb) {
-  const uint32_t per = nb >> 1;
-  return b < (per << 1) ? (b & 1u) * per + (b >> 1) : b;
-}
-
 struct ProbeArgs {
   const uint8_t* src[kMaxStreams];
   uint8_t* dst[kMaxStreams];
@@ -46,8 +39,7 @@ struct ProbeArgs {
 template <int R, int W>
 __global__ void __launch_bounds__(kBlock) probe_kernel(const ProbeArgs a) {
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)split_tile(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
-       idx < a.n16; idx += stride) {
+  for (uint64_t idx = (uint64_t)blockIdx.x * kBlock + threadIdx.x; idx < a.n16; idx += stride) {
     u32x4 acc = {(uint32_t)idx, 0x9e3779b9u, 0x7f4a7c15u, 0x85ebca6bu};
 #pragma unroll
     for (int j = 0; j < R; ++j) acc ^= load_nt(a.src[j] + idx * 16);
@@ -65,7 +57,7 @@ __global__ void __launch_bounds__(kBlock) probe_kernel(const ProbeArgs a) {
 template <int R, int W>
 int launch(const ProbeArgs& a, hipStream_t st) {
   const uint64_t tiles = (a.n16 + kBlock - 1) / kBlock;
-  const unsigned grid = (unsigned)(tiles < (1u << 20) ? (tiles ? tiles : 1) : (1u << 20));
+  const unsigned grid = (unsigned)(tiles < (1u << 24) ? (tiles ? tiles : 1) : (1u << 24));
   hipLaunchKernelGGL((probe_kernel<R, W>), dim3(grid), dim3(kBlock), 0, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -76,7 +68,7 @@ int launch(const ProbeArgs& a, hipStream_t st) {
 // log (256 B) and exp (512 B, doubled so the sum needs no reduction) in LDS.
 // Per data byte: one log lookup shared by the m outputs and one exp lookup
 // per output, all byte-granular LDS reads at data-dependent addresses.  Same
-// grid, tile order and non-temporal 16-byte loads and stores as rs_kernel.
+// workgroups, grid and non-temporal 16-byte loads and stores as rs_kernel.
 struct LogExpArgs {
   const uint8_t* src[kMaxStreams];
   uint8_t* dst[kMaxStreams];
@@ -98,8 +90,7 @@ __global__ void __launch_bounds__(kBlock) logexp_kernel(const LogExpArgs a) {
                                                      threadIdx.x % K];
   __syncthreads();
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)split_tile(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
-       idx < a.n16; idx += stride) {
+  for (uint64_t idx = (uint64_t)blockIdx.x * kBlock + threadIdx.x; idx < a.n16; idx += stride) {
     u32x4 acc[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) acc[i] = u32x4{0u, 0u, 0u, 0u};
@@ -168,7 +159,7 @@ int ecp_rs_logexp(const uint8_t* coeff, int k, int m, const uint8_t* const* src,
   a.n16 = nbytes / 16;
   if (a.n16 == 0) return 0;
   const uint64_t tiles = (a.n16 + kBlock - 1) / kBlock;
-  const unsigned grid = (unsigned)(tiles < (1u << 20) ? tiles : (1u << 20));
+  const unsigned grid = (unsigned)(tiles < (1u << 24) ? tiles : (1u << 24));
   hipLaunchKernelGGL((logexp_kernel<6, 3>), dim3(grid), dim3(kBlock), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? 0 : -4;
