@@ -202,13 +202,15 @@ def cpu_batched(coeff, hptr, hlen, stripes, unit: int, gpu_parity, seconds: floa
     return res
 
 
-def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: float = 0.0) -> dict:
+def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: float = 0.0,
+                    with_checkpoint: bool = True) -> dict:
     """Configs 4 and 5 through the batched stripe launcher: data GB/s of one
     launch (HIP events) and HBM traffic GB/s, with product-only checks (a
     decode round trip; update == full re-encode).  The bytes are drawn on
     the host (numpy, seeded, on the box's cores) and uploaded; with
     ``cpu_seconds`` the repo's CPU encoder is timed on sampled stripes of the
-    same host bytes (key "cpu")."""
+    same host bytes (key "cpu").  ``with_checkpoint`` adds the checkpoint
+    staging and snapshot measurements on config 5's tensors."""
     import numpy as np
     import torch
     from megatron_lm_amd.layout import stripe_descriptors
@@ -292,12 +294,35 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     lost = [1, 7, 12, 14]
     dplan = lay.plan_decode(par, lost)
     w, e = timed(lambda: lay.run(dplan), 5, 1)
+    k5, S5, U5 = 12, lay.n_stripes, 64 << 10
+    surv = [p for p in range(16) if p not in lost][:k5]
+    hl = lay.host_len.astype(np.int64)
+    dec_traffic = sum(int(hl[:, p].sum()) if p < k5 else S5 * U5 for p in surv + lost)
     out["rs124_ragged_decode4_GBps"] = round(lay.data_bytes / (e * 1e-3) / 1e9, 1)
+    out["rs124_ragged_decode4_traffic_GBps"] = round(dec_traffic / (e * 1e-3) / 1e9, 1)
     log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
-    del lay, par, olds, plan, dplan
+    del olds, plan, dplan
+    # the snapshot's kernel: encode plus a zero-padded copy of every data
+    # unit into one (16, stripes, 64 KiB) block, one pass over the data
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    block = torch.empty((16, S5, U5), dtype=torch.uint8, device=dev)
+    bp, gp = GpuSliceCodec._row_ptrs(block, 12, 4), GpuSliceCodec._row_ptrs(block, 0, 12)
+    L, st = pkg._lib.lib(), pkg.codec.stream_handle(None, dev)
+
+    def copy_encode():
+        pkg._lib.check(L.ec_encode_batched_copy(
+            pkg._lib.u8ptr(lay.coeff), 12, 4, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+            bp.data_ptr(), gp.data_ptr(), S5, U5, st), "ec_encode_batched_copy")
+    w, e = timed(copy_encode, 5, 1)
+    out["rs124_ragged_copy_encode_traffic_GBps"] = round((lay.data_bytes + block.numel()) /
+                                                        (e * 1e-3) / 1e9, 1)
+    out["rs124_ragged_copy_encode_ms"] = round(e, 3)
+    log(f"copying encode {out['rs124_ragged_copy_encode_traffic_GBps']} GB/s of traffic")
+    del lay, par, block, bp, gp
     torch.cuda.empty_cache()
-    out.update(checkpoint_staging(pkg, tensors))
-    out.update(checkpoint_snapshot(pkg, tensors, gemm))
+    if with_checkpoint:
+        out.update(checkpoint_staging(pkg, tensors))
+        out.update(checkpoint_snapshot(pkg, tensors, gemm))
     del tensors
     torch.cuda.empty_cache()
     if cpu:
@@ -571,24 +596,75 @@ def ragged_tensors(synth, dev, seed: int, with_host: bool = False):
 
 
 def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
-    """Counter-run workload for the batched launcher: the 256 MiB streaming
-    copy (calibration, 3 launches) then 3 launches of the config-5 encode."""
+    """Counter-run workload for the batched launcher, three launches each, in
+    this order: the engine's streaming copy of one 256 MiB shard (the
+    calibration kernel of known traffic); config 5 (RS(12,4), 3,000 ragged
+    tensors, 64 KiB units): encode, copying encode into one (16, stripes,
+    64 KiB) block (the snapshot's kernel), decode of lost positions 1, 7, 12,
+    14, 1 % update; config 4 (RS(8,2), 20.8 GB buffer, 4 MiB units) encode.
+    Prints the launch groups with their algorithmic bytes as JSON."""
+    import numpy as np
     import torch
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    groups = []
+
+    def three(name, fn, read, write):
+        torch.cuda.synchronize()
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        groups.append({"name": name, "launches": 3, "read_bytes": int(read),
+                       "write_bytes": int(write)})
+
     shard = 256 * MiB
     src = torch.empty(shard, dtype=torch.uint8, device=dev).random_(0, 256)
     dst = torch.empty_like(src)
-    for _ in range(3):
-        pkg.xor_encode([src], out=dst)
-    torch.cuda.synchronize()
-    lay = pkg.StripeLayout(ragged_tensors(synth, dev, seed), 12, 4, 64 << 10)
+    three("copy", lambda: pkg.xor_encode([src], out=dst), shard, shard)
+    del src, dst
+    tensors = ragged_tensors(synth, dev, seed)
+    k, m, U = 12, 4, 64 << 10
+    lay = pkg.StripeLayout(tensors, k, m, U)
     par = lay.alloc_parity()
-    for _ in range(3):
-        lay.encode(par)
-    torch.cuda.synchronize()
-    print(json.dumps({"mode": "batched-pmc", "copy_bytes_read": shard,
-                      "copy_bytes_written": shard, "data_bytes": lay.data_bytes,
-                      "parity_bytes": par.numel(), "n_units": lay.n_units,
-                      "n_stripes": lay.n_stripes}), flush=True)
+    S = lay.n_stripes
+    valid = lay.data_bytes
+    three("c5_encode", lambda: lay.encode(par), valid, par.numel())
+    block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
+    pp = GpuSliceCodec._row_ptrs(block, k, m)
+    gp = GpuSliceCodec._row_ptrs(block, 0, k)
+    L = pkg._lib.lib()
+    st = pkg.codec.stream_handle(None, dev)
+
+    def copy_encode():
+        pkg._lib.check(L.ec_encode_batched_copy(
+            pkg._lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+            pp.data_ptr(), gp.data_ptr(), S, U, st), "ec_encode_batched_copy")
+    three("c5_copy_encode", copy_encode, valid, block.numel())
+    del block, pp, gp
+    three("c5_encode_again", lambda: lay.encode(par), valid, par.numel())
+    lost = [1, 7, 12, 14]
+    dplan = lay.plan_decode(par, lost)
+    # survivors: data positions 0, 2-6, 8-11 and parity 13, 15 of every stripe;
+    # outputs: the valid bytes of data positions 1 and 7, parity 12 and 14
+    surv = [p for p in range(k + m) if p not in lost][:k]
+    hl = lay.host_len.astype(np.int64)
+    read = sum(int(hl[:, p].sum()) if p < k else S * U for p in surv)
+    write = sum(int(hl[:, p].sum()) if p < k else S * U for p in lost)
+    three("c5_decode4", lambda: lay.run(dplan), read, write)
+    changed = synth.perturbed_units(seed, lay.n_units, 0.01)
+    olds = [lay.unit_view(u).clone() for u in changed.tolist()]
+    uplan = lay.plan_update(par, changed, olds)
+    cb = int(lay.host_len.reshape(-1)[changed].sum())
+    three("c5_update", lambda: lay.run(uplan), 2 * cb + uplan.n_stripes * m * U,
+          uplan.n_stripes * m * U)
+    del lay, par, dplan, uplan, olds, tensors
+    torch.cuda.empty_cache()
+    host = synth.gpt_rank_buffer_host(seed)
+    buf = torch.from_numpy(host).to(dev)
+    del host
+    lay = pkg.StripeLayout([buf], 8, 2, 4 * MiB)
+    par = lay.alloc_parity()
+    three("c4_encode", lambda: lay.encode(par), lay.data_bytes, par.numel())
+    print(json.dumps({"mode": "batched-pmc", "groups": groups}), flush=True)
     return 0
 
 
@@ -774,14 +850,16 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
-    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched", "batched-pmc",
-                                       "gf-variants", "train"],
+    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched",
+                                       "batched-kernels", "batched-pmc", "gf-variants", "train"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); pmc: a few launches of a "
                          "plain 256 MiB copy and of the RS(6,3) encode, for counter runs; "
-                         "batched: configs 4 and 5 only; batched-pmc: the copy plus 3 "
-                         "launches of the config-5 encode, for counter runs; gf-variants: "
+                         "batched: configs 4 and 5 only; batched-kernels: the same without "
+                         "the checkpoint staging and snapshot (for kernel-trace profiles); "
+                         "batched-pmc: the copy plus 3 launches of each batched kernel, for "
+                         "counter runs; gf-variants: "
                          "the v_perm GF multiply against LDS log/exp tables; train: a training "
                          "loop with synchronous and with snapshot checkpoint saves")
     args = ap.parse_args()
@@ -801,9 +879,10 @@ def main() -> int:
 
     if args.mode == "pmc":
         return pmc_launches(pkg, dev)
-    if args.mode == "batched":
-        print(json.dumps({"mode": "batched",
-                          **batched_configs(pkg, synth, dev, args.seed, GemmLoad(dev))}),
+    if args.mode in ("batched", "batched-kernels"):
+        print(json.dumps({"mode": args.mode,
+                          **batched_configs(pkg, synth, dev, args.seed, GemmLoad(dev),
+                                            with_checkpoint=args.mode == "batched")}),
               flush=True)
         return 0
     if args.mode == "batched-pmc":
@@ -931,7 +1010,7 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(enc_traffic_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(k, m, shard),
-                     "kernel": "rs_kernel<6,3,1>",
+                     "kernel": "rs_kernel<6,3>",
                      "algorithmic_bytes_per_launch": traffic,
                      "kernel_us": round(ev_ms * 1e3, 2),
                      "settle_ms": round(settle_ms, 1),

@@ -21,7 +21,7 @@ struct UpdateArgs {
   const uint64_t* pptr;  // [n_stripes][M]
   PermTab tab[M][K];
   uint32_t unit_bytes;
-  uint32_t tiles_per_unit;   // tiles of kBlock*16 bytes in a unit
+  uint32_t tiles_per_unit;   // tiles of B*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;
 };
@@ -31,8 +31,8 @@ struct UpdateArgs {
 // and new bytes are, their lengths) are read once per span into scalar
 // registers; a tile inside every changed unit, with everything 16-byte
 // aligned, takes plain vector loads, any other tile the byte-granular path.
-template <int K, int M>
-__global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a) {
+template <int K, int M, int B>
+__global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
   const uint32_t s = blockIdx.x / a.blocks_per_unit;
@@ -66,9 +66,9 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
     aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
   }
   for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t off = (t * kBlock + threadIdx.x) * 16u;
+    const uint32_t off = (t * B + threadIdx.x) * 16u;
     if (off >= a.unit_bytes) continue;
-    const bool fast = aligned && (t + 1) * (kBlock * 16u) <= full;
+    const bool fast = aligned && (t + 1) * (B * 16u) <= full;
     uint32_t acc[M][4] = {};
     // The parity loads do not depend on the delta: issue them first so that
     // they are in flight together with the unit loads.
@@ -123,7 +123,6 @@ __global__ void __launch_bounds__(kBlock) update_kernel(const UpdateArgs<K, M> a
 // its stripe's descriptors and the m x k tables in LDS; fast tiles issue the
 // unit loads in groups of kWideGroup, edge tiles take the units one at a
 // time with byte-granular ends, as in the fixed-size kernels.
-constexpr uint32_t kWideTile = kBlock * 16u;
 
 struct BatchWideArgs {
   const uint64_t* dptr;  // [n_stripes][k] (update: new units, 0 = unchanged)
@@ -151,12 +150,15 @@ struct WideStripe {
 
 // Tables and stripe s's descriptors into LDS.  Returns, after a barrier,
 // whether any unit or output address is not 16-byte aligned (uniform).
-template <int M>
+// Lanes 0..k-1 read the data descriptors, lanes 32..32+M-1 the parity ones
+// (k <= 32, M <= 16): B >= 64.
+template <int M, int B>
 __device__ __forceinline__ bool stage_wide(WideStripe<M>& w, const BatchWideArgs& a, uint32_t s,
                                            bool update) {
+  static_assert(B >= 64, "stage_wide needs lanes 0..47");
   const int k = a.k;
   const uint32_t t = threadIdx.x;
-  for (uint32_t i = t; i < (uint32_t)(M * k); i += kBlock) w.tab[i] = dev_perm_tab(a.coeff[i]);
+  for (uint32_t i = t; i < (uint32_t)(M * k); i += B) w.tab[i] = dev_perm_tab(a.coeff[i]);
   if (t < (uint32_t)k) {
     const uint8_t* d = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * k + t]);
     const uint32_t l = d ? a.dlen[(uint64_t)s * k + t] : 0u;
@@ -165,8 +167,8 @@ __device__ __forceinline__ bool stage_wide(WideStripe<M>& w, const BatchWideArgs
     w.d[t] = d;
     w.o[t] = o;
     w.len[t] = l < a.unit_bytes ? l : a.unit_bytes;
-  } else if (t >= 64 && t < 64 + M) {
-    const uint32_t i = t - 64;
+  } else if (t >= 32 && t < 32 + M) {
+    const uint32_t i = t - 32;
     uint8_t* p = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
     const uint32_t l = p ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
     w.p[i] = p;
@@ -196,13 +198,14 @@ __device__ __forceinline__ void wide_mac(uint32_t (&acc)[M][4], const uint4& x,
   }
 }
 
-template <int M>
-__global__ void __launch_bounds__(kBlock) batched_wide_kernel(const BatchWideArgs a) {
+template <int M, int B>
+__global__ void __launch_bounds__(B) batched_wide_kernel(const BatchWideArgs a) {
+  constexpr uint32_t kWideTile = B * 16u;
   __shared__ WideStripe<M> w;
   const uint32_t s = blockIdx.x / a.blocks_per_unit;
   const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
-  const bool misaligned = stage_wide<M>(w, a, s, false);
+  const bool misaligned = stage_wide<M, B>(w, a, s, false);
   const int k = a.k;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t lo = t * kWideTile, hi = lo + kWideTile;
@@ -246,13 +249,14 @@ __global__ void __launch_bounds__(kBlock) batched_wide_kernel(const BatchWideArg
 }
 
 // parity[s][i] ^= C[i][j] * (new[s][j] ^ old[s][j]) for the changed units.
-template <int M>
-__global__ void __launch_bounds__(kBlock) update_wide_kernel(const BatchWideArgs a) {
+template <int M, int B>
+__global__ void __launch_bounds__(B) update_wide_kernel(const BatchWideArgs a) {
+  constexpr uint32_t kWideTile = B * 16u;
   __shared__ WideStripe<M> w;
   const uint32_t s = blockIdx.x / a.blocks_per_unit;
   const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
-  stage_wide<M>(w, a, s, true);
+  stage_wide<M, B>(w, a, s, true);
   const int k = a.k;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t off = t * kWideTile + threadIdx.x * 16u;
@@ -276,7 +280,7 @@ __global__ void __launch_bounds__(kBlock) update_wide_kernel(const BatchWideArgs
   }
 }
 
-template <int K, int M>
+template <int K, int M, int B = kBlock>
 int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* optr,
                   const uint32_t* len, const uint64_t* pptr, uint32_t n_stripes,
                   uint32_t unit_bytes, hipStream_t st) {
@@ -289,7 +293,7 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   const uint32_t unit16 = unit_bytes / 16u;
   a.unit_bytes = unit_bytes;
-  a.tiles_per_unit = (unit16 + kBlock - 1) / kBlock;
+  a.tiles_per_unit = (unit16 + B - 1) / B;
   // One tile per workgroup: each tile is a dependent chain (unit and parity
   // loads, then the parity store), so the update wants as many workgroups
   // in flight as it has tiles.  Measured for the 1 % update of 3,000 ragged
@@ -304,18 +308,19 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
-  hipLaunchKernelGGL((update_kernel<K, M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+  hipLaunchKernelGGL((update_kernel<K, M, B>), dim3((unsigned)blocks), dim3(B), 0, st, a);
   return hip_status();
 }
 
 // Wide codes through the batched kernels: encode / decode (update = false,
-// optr unused) or the parity update.  The same span rules as the fixed-size
-// launchers: spans of span_bytes() with at least 2048 workgroups for the
-// encode, one tile per workgroup for the update.
-template <int M>
-int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
-                        const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
-                        uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st) {
+// optr unused) or the parity update, with B-lane workgroups on B * 16-byte
+// tiles: the encode walks spans of `span` bytes (0: span_bytes()) keeping at
+// least 2048 workgroups, the update one tile per workgroup.
+template <int M, int B>
+int launch_batched_wide_b(const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
+                          const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
+                          uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st,
+                          uint32_t span) {
   BatchWideArgs a;
   a.dptr = dptr;
   a.dlen = dlen;
@@ -325,11 +330,12 @@ int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const
   for (int t = 0; t < M * k; ++t) a.coeff[t] = coeff[t];
   a.k = k;
   a.unit_bytes = unit_bytes;
-  a.tiles_per_unit = (unit_bytes / 16u + kBlock - 1) / kBlock;
+  a.tiles_per_unit = (unit_bytes / 16u + B - 1) / B;
   const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
   uint64_t tpb = 1;
   if (!update) {
-    tpb = span_bytes(unit_bytes) / kWideTile;
+    tpb = (span ? span : span_bytes(unit_bytes)) / (B * 16u);
+    if (tpb < 1) tpb = 1;
     if (total_tiles / tpb < 2048) tpb = total_tiles / 2048;
   } else {
     tpb = (total_tiles + 0x3fffffffull) >> 30;
@@ -341,10 +347,28 @@ int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
   if (update)
-    hipLaunchKernelGGL((update_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((update_wide_kernel<M, B>), dim3((unsigned)blocks), dim3(B), 0, st, a);
   else
-    hipLaunchKernelGGL((batched_wide_kernel<M>), dim3((unsigned)blocks), dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((batched_wide_kernel<M, B>), dim3((unsigned)blocks), dim3(B), 0, st, a);
   return hip_status();
+}
+
+// Encode and decode with m <= 4 run one-wavefront workgroups on one 1 KiB
+// tile each, like the fixed-size batched kernel; wider outputs and the update
+// keep 256-lane workgroups.  Measured on MI355X (HBM traffic, GB/s, 8 GiB
+// buffers): RS(20,4) over 4 MiB units encode 5041 -> 5314, decode of 4
+// positions 4886 -> 5136; with m >= 6 the per-workgroup table build (m * k
+// tables) made one-wavefront workgroups 5 % slower (RS(16,6) over 64 KiB
+// units 4995 -> 4747, RS(24,8) over 1 MiB units 3980 -> 3815).
+template <int M>
+int launch_batched_wide(const uint8_t* coeff, int k, const uint64_t* dptr, const uint32_t* dlen,
+                        const uint64_t* optr, const uint64_t* pptr, const uint32_t* olen,
+                        uint32_t n_stripes, uint32_t unit_bytes, bool update, hipStream_t st) {
+  if (M <= 4 && !update)
+    return launch_batched_wide_b<M, 64>(coeff, k, dptr, dlen, optr, pptr, olen, n_stripes,
+                                        unit_bytes, update, st, 64 * 16);
+  return launch_batched_wide_b<M, kBlock>(coeff, k, dptr, dlen, optr, pptr, olen, n_stripes,
+                                          unit_bytes, update, st, 0);
 }
 
 using UpdFn = int (*)(const uint8_t*, const uint64_t*, const uint64_t*, const uint32_t*,
