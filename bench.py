@@ -303,10 +303,11 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
     del olds, plan, dplan
     # the snapshot's kernel: encode plus a zero-padded copy of every data
-    # unit into one (16, stripes, 64 KiB) block, one pass over the data
+    # unit into one stripe-major (stripes, 16, 64 KiB) block, one pass over
+    # the data
     from megatron_lm_amd.checkpoint import GpuSliceCodec
-    block = torch.empty((16, S5, U5), dtype=torch.uint8, device=dev)
-    bp, gp = GpuSliceCodec._row_ptrs(block, 12, 4), GpuSliceCodec._row_ptrs(block, 0, 12)
+    block = torch.empty((S5, 16, U5), dtype=torch.uint8, device=dev)
+    bp, gp = GpuSliceCodec._unit_ptrs(block, 12, 4), GpuSliceCodec._unit_ptrs(block, 0, 12)
     L, st = pkg._lib.lib(), pkg.codec.stream_handle(None, dev)
 
     def copy_encode():
@@ -628,9 +629,9 @@ def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
     S = lay.n_stripes
     valid = lay.data_bytes
     three("c5_encode", lambda: lay.encode(par), valid, par.numel())
-    block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
-    pp = GpuSliceCodec._row_ptrs(block, k, m)
-    gp = GpuSliceCodec._row_ptrs(block, 0, k)
+    block = torch.empty((S, k + m, U), dtype=torch.uint8, device=dev)
+    pp = GpuSliceCodec._unit_ptrs(block, k, m)
+    gp = GpuSliceCodec._unit_ptrs(block, 0, k)
     L = pkg._lib.lib()
     st = pkg.codec.stream_handle(None, dev)
 

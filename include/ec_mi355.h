@@ -253,6 +253,29 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                      uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
                      uint64_t pinned_bytes, int threads, ec_stream_t stream);
 
+/* Copies a stripe-major device block of n_stripes x positions units of
+ * unit_bytes (unit (s, p) at d_block + (s * positions + p) * unit_bytes) to
+ * one host row per position: unit (s, p) goes to h_rows[p] + s * unit_bytes,
+ * so row p receives position p of every stripe, back to back (n_stripes *
+ * unit_bytes bytes; need not be pinned).  The block moves in contiguous
+ * chunks of half the caller's pinned buffer, one transfer each on `stream`,
+ * while `threads` host threads scatter the previous chunk's units into the
+ * rows.  Returns when every byte is in its row; the transfers follow the
+ * work already enqueued on `stream`.  EC_EINVAL for null pointers (any
+ * h_rows[p] included), threads outside [1, 64], a pinned buffer under 2
+ * bytes, or a block size that overflows 64 bits; n_stripes, positions or
+ * unit_bytes 0 is a no-op.  The stream advice of ec_stage_to_host applies.
+ * No counterpart in the reference (as for ec_stage_to_host: its checkpoint
+ * D2H is copy_tensors_to_cpu, tensor_aware_state_dict.py:245-274).  This is
+ * the staging of the block ec_encode_batched_copy writes stripe-major: there
+ * the k + m output units of a stripe are adjacent in HBM, which that kernel
+ * writes measurably faster than k + m rows each S units long (on MI355X,
+ * RS(12,4) over 26,266 stripes of 64 KiB units: 0.79 against 0.74 of the
+ * HBM roofline). */
+int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_t positions,
+                             uint64_t unit_bytes, uint8_t* const* h_rows, uint8_t* h_pinned,
+                             uint64_t pinned_bytes, int threads, ec_stream_t stream);
+
 /* The way back: row r of a rows x row_bytes region, read from the host
  * array h_rows[r] (need not be pinned; a host array of row_bytes bytes
  * each), goes to d_dst + r * dst_pitch in device memory, through the

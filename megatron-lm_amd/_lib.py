@@ -41,6 +41,7 @@ EXPORTS = (
     "ec_stream_create",
     "ec_stream_destroy",
     "ec_stage_to_host",
+    "ec_stage_stripes_to_host",
     "ec_stage_to_device",
 )
 
@@ -112,6 +113,8 @@ def lib() -> ctypes.CDLL:
     L.ec_stream_destroy.argtypes = [_vp]
     L.ec_stage_to_host.restype = _i
     L.ec_stage_to_host.argtypes = [_vp, _u64, _vp, _u64, _u32, _u64, _vp, _u64, _i, _vp]
+    L.ec_stage_stripes_to_host.restype = _i
+    L.ec_stage_stripes_to_host.argtypes = [_vp, _u32, _u32, _u64, _vp, _vp, _u64, _i, _vp]
     L.ec_stage_to_device.restype = _i
     L.ec_stage_to_device.argtypes = [_vp, _u32, _u64, _vp, _u64, _vp, _u64, _i, _vp]
     _lib = L

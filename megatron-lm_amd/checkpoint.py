@@ -184,7 +184,7 @@ class GpuSliceCodec:
     rows of one pageable host array.
 
     ``encode`` codes the state into one (k + m) / k block in HBM when that
-    fits (see ``snapshot``) and stages it with ``ec_stage_to_host``;
+    fits (see ``snapshot``) and stages it with ``ec_stage_stripes_to_host``;
     otherwise the work goes in chunks of stripes of at most ``chunk_bytes``,
     double-buffered on the device and in pinned host memory: 2 * chunk_bytes
     of extra HBM and of page-locked memory.  ``decode`` likewise takes one
@@ -264,15 +264,16 @@ class GpuSliceCodec:
         return np.uint64(block[p].data_ptr()) + np.arange(S, dtype=np.uint64) * np.uint64(U)
 
     @staticmethod
-    def _row_ptrs(block: torch.Tensor, first: int, count: int) -> torch.Tensor:
-        """[stripes, count] device addresses of the units of rows first ..
-        first + count - 1 of a (rows, stripes, unit_bytes) device block,
-        computed on the device (no host array, no upload)."""
-        _, S, U = block.shape
-        stripe = torch.arange(S, dtype=torch.int64, device=block.device).unsqueeze(1) * U
-        row = torch.arange(first, first + count, dtype=torch.int64,
-                           device=block.device).unsqueeze(0) * (S * U)
-        return (stripe + row).add_(block.data_ptr())
+    def _unit_ptrs(block: torch.Tensor, first: int, count: int) -> torch.Tensor:
+        """[stripes, count] device addresses of positions first .. first +
+        count - 1 of every stripe of a stripe-major (stripes, positions,
+        unit_bytes) device block, computed on the device (no host array, no
+        upload)."""
+        S, P, U = block.shape
+        stripe = torch.arange(S, dtype=torch.int64, device=block.device).unsqueeze(1) * (P * U)
+        pos = torch.arange(first, first + count, dtype=torch.int64,
+                           device=block.device).unsqueeze(0) * U
+        return (stripe + pos).add_(block.data_ptr())
 
     @staticmethod
     def _dev(a: np.ndarray, dt, device) -> torch.Tensor:
@@ -393,8 +394,8 @@ class GpuSliceCodec:
         return self._meta(lay, tensors), [out[p] for p in range(k + m)]
 
     def snapshot(self, tensors: Sequence[torch.Tensor], hold: bool = True) -> "PendingSlices":
-        """Code the tensors into one (k + m, stripes, unit_bytes) block in HBM
-        and stage it to host memory in the background.
+        """Code the tensors into one stripe-major (stripes, k + m, unit_bytes)
+        block in HBM and stage it to host memory in the background.
 
         One launch (parity plus the copy of every data unit, one read of the
         data) runs on the device's side stream (its own hardware queue) after
@@ -402,8 +403,11 @@ class GpuSliceCodec:
         current stream then waits for it, so later work there (the next
         optimizer step) cannot change the tensors before they are coded.  That
         wait is the whole stall of a save: the block is (k + m) / k of the
-        state in HBM, written at HBM speed.  A background thread moves the
-        block to host memory as ``encode`` does and frees it;
+        state in HBM, written at HBM speed (stripe-major, so that the k + m
+        units a workgroup writes are adjacent: faster than k + m separate
+        rows).  A background thread moves the block to host memory, one
+        (k + m, stripes * unit_bytes) host array whose row p is slice p, and
+        frees it;
         ``PendingSlices.result()`` returns ``(meta, slices)`` as ``encode``
         would.  Without ``hold`` the caller must order its own writes after
         ``PendingSlices.coded``.
@@ -425,7 +429,7 @@ class GpuSliceCodec:
         if (k + m) * S * U <= self._snapshot_limit(dev):
             try:
                 with torch.cuda.device(dev):
-                    block = torch.empty((k + m, S, U), dtype=torch.uint8, device=dev)
+                    block = torch.empty((S, k + m, U), dtype=torch.uint8, device=dev)
             except torch.OutOfMemoryError:
                 block = None
         if block is None:
@@ -435,8 +439,8 @@ class GpuSliceCodec:
             return PendingSlices(coded, ready=ready)
         side = side_stream(dev)
         with torch.cuda.device(dev):
-            pp = self._row_ptrs(block, k, m)
-            gp = self._row_ptrs(block, 0, k)
+            pp = self._unit_ptrs(block, k, m)
+            gp = self._unit_ptrs(block, 0, k)
         for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
             t.record_stream(side)
         side.wait_stream(cur)   # the tensors' producers and the descriptor uploads
@@ -464,10 +468,11 @@ class GpuSliceCodec:
                 xfer = torch.cuda.Stream(dev)
                 xfer.wait_event(coded)
                 block.record_stream(xfer)
-                _lib.check(_lib.lib().ec_stage_to_host(
-                    block.data_ptr(), S * U, out.ctypes.data, S * U, k + m, S * U,
+                _lib.check(_lib.lib().ec_stage_stripes_to_host(
+                    block.data_ptr(), S, k + m, U,
+                    _lib.ptr_array([out[p].ctypes.data for p in range(k + m)]),
                     pinned.data_ptr(), pinned.numel(), self.stage_threads,
-                    stream_handle(xfer, dev)), "ec_stage_to_host")
+                    stream_handle(xfer, dev)), "ec_stage_stripes_to_host")
             block = None   # back to the allocator: the last transfer has landed
             return meta, [out[p] for p in range(k + m)]
 

@@ -69,4 +69,20 @@ void gather_rows(uint8_t* dst, const uint8_t* const* src_rows, uint64_t x0, uint
   });
 }
 
+void scatter_units(uint8_t* const* dst_rows, uint32_t positions, uint64_t unit, uint64_t x0,
+                   const uint8_t* src, uint64_t len, int threads) {
+  if (len == 0 || unit == 0 || positions == 0 || threads < 1) return;
+  const uint64_t share = (len + threads - 1) / threads;
+  run_shares(threads, [&](int t) {
+    uint64_t b = (uint64_t)t * share;
+    const uint64_t e = std::min(len, b + share);
+    while (b < e) {
+      const uint64_t g = x0 + b, u = g / unit, off = g % unit;
+      const uint64_t n = std::min(e - b, unit - off);
+      memcpy(dst_rows[u % positions] + (u / positions) * unit + off, src + b, n);
+      b += n;
+    }
+  });
+}
+
 }  // namespace ec

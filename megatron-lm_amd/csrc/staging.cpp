@@ -1,5 +1,6 @@
 // staging.cpp — host side of moving coded checkpoint slices out of HBM
-// (ec_stage_to_host) and back in (ec_stage_to_device); the host copies are
+// (ec_stage_to_host for row-major regions, ec_stage_stripes_to_host for a
+// stripe-major block) and back in (ec_stage_to_device); the host copies are
 // in host_copy.cpp.
 //
 // A background save stages the coded block to host memory while training
@@ -21,6 +22,60 @@
 #include "ec_mi355.h"
 #include "host_copy.h"
 
+namespace {
+
+// The stream's device made current for the call (the events belong on it,
+// whichever device the calling thread has current) and the two events that
+// mark the pinned halves; undone on every return.
+struct Session {
+  hipStream_t st;
+  int prev = 0;
+  bool switched = false;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  int status = EC_OK;
+
+  explicit Session(ec_stream_t stream) : st(reinterpret_cast<hipStream_t>(stream)) {
+    hipDevice_t sdev = 0;
+    if (hipGetDevice(&prev) != hipSuccess || (st && hipStreamGetDevice(st, &sdev) != hipSuccess)) {
+      status = EC_EHIP;
+      return;
+    }
+    switched = st && sdev != prev;
+    if (switched && hipSetDevice(sdev) != hipSuccess) {
+      switched = false;
+      status = EC_EHIP;
+      return;
+    }
+    for (auto& e : ev)
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
+        status = EC_EHIP;
+  }
+  ~Session() {
+    for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (switched) (void)hipSetDevice(prev);
+  }
+  bool ok() const { return status == EC_OK; }
+  void fail() { status = EC_EHIP; }
+  // Marks pinned half h as filled by what is enqueued so far.
+  void mark(int h) {
+    if (ok() && hipEventRecord(ev[h], st) != hipSuccess) fail();
+  }
+  // Waits until the transfers marked on half h have landed.
+  void wait(int h) {
+    if (ok() && hipEventSynchronize(ev[h]) != hipSuccess) fail();
+  }
+};
+
+// Bytes per pinned half: whole pages when there is room.
+uint64_t half_of(uint64_t pinned_bytes, uint64_t per_byte_rows) {
+  uint64_t w = pinned_bytes / 2 / per_byte_rows;
+  if (w >= 4096) w -= w % 4096;
+  return w;
+}
+
+}  // namespace
+
 extern "C" {
 
 int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
@@ -31,52 +86,70 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
   if (src_pitch < row_bytes || dst_pitch < row_bytes) return EC_EINVAL;
   // Two halves of the pinned buffer, each holding `width` bytes of every row.
   const uint64_t half = pinned_bytes / 2;
-  uint64_t width = half / rows;
-  if (width >= 4096) width -= width % 4096;  // whole pages when there is room
+  uint64_t width = half_of(pinned_bytes, rows);
   if (width == 0) return EC_EINVAL;
   width = std::min(width, row_bytes);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // The events belong on the stream's device, whichever device the calling
-  // thread has current.
-  int prev = 0;
-  hipDevice_t sdev = 0;
-  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
-  if (st && hipStreamGetDevice(st, &sdev) != hipSuccess) return EC_EHIP;
-  const bool switched = st && sdev != prev;
-  if (switched && hipSetDevice(sdev) != hipSuccess) return EC_EHIP;
-  hipEvent_t ev[2] = {nullptr, nullptr};
-  int status = EC_OK;
-  for (auto& e : ev)
-    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
-      status = EC_EHIP;
+  Session ss(stream);
   const uint64_t n_chunks = (row_bytes + width - 1) / width;
   // Chunk j: columns [j * width, min(row_bytes, (j + 1) * width)) of every
   // row, through pinned half j % 2.  The transfer of chunk j is in flight
   // while the threads copy chunk j - 1 out of the other half.
-  for (uint64_t j = 0; status == EC_OK && j <= n_chunks; ++j) {
+  for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
     if (j < n_chunks) {
       const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
       uint8_t* pin = h_pinned + (j % 2) * half;
-      for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
+      for (uint32_t r = 0; r < rows && ss.ok(); ++r)
         if (hipMemcpyAsync(pin + (uint64_t)r * w, d_src + (uint64_t)r * src_pitch + x0, w,
-                           hipMemcpyDeviceToHost, st) != hipSuccess)
-          status = EC_EHIP;
-      if (status == EC_OK && hipEventRecord(ev[j % 2], st) != hipSuccess) status = EC_EHIP;
+                           hipMemcpyDeviceToHost, ss.st) != hipSuccess)
+          ss.fail();
+      ss.mark(j % 2);
     }
-    if (status == EC_OK && j >= 1) {
+    if (j >= 1) {
       const uint64_t p = j - 1, x0 = p * width, w = std::min(width, row_bytes - x0);
-      if (hipEventSynchronize(ev[p % 2]) != hipSuccess) {
-        status = EC_EHIP;
-        break;
-      }
+      ss.wait(p % 2);
+      if (!ss.ok()) break;
       ec::copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
     }
   }
-  if (status != EC_OK) (void)hipStreamSynchronize(st);  // no transfer outlives the call
-  for (auto& e : ev)
-    if (e) (void)hipEventDestroy(e);
-  if (switched) (void)hipSetDevice(prev);
-  return status;
+  if (!ss.ok()) (void)hipStreamSynchronize(ss.st);  // no transfer outlives the call
+  return ss.status;
+}
+
+int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_t positions,
+                             uint64_t unit_bytes, uint8_t* const* h_rows, uint8_t* h_pinned,
+                             uint64_t pinned_bytes, int threads, ec_stream_t stream) {
+  if (n_stripes == 0 || positions == 0 || unit_bytes == 0) return EC_OK;
+  if (!d_block || !h_rows || !h_pinned || threads < 1 || threads > 64) return EC_EINVAL;
+  for (uint32_t p = 0; p < positions; ++p)
+    if (!h_rows[p]) return EC_EINVAL;
+  const uint64_t units = (uint64_t)n_stripes * positions;
+  if (unit_bytes > UINT64_MAX / units) return EC_EINVAL;
+  const uint64_t total = units * unit_bytes, half = pinned_bytes / 2;
+  uint64_t width = half_of(pinned_bytes, 1);
+  if (width == 0) return EC_EINVAL;
+  width = std::min(width, total);
+  Session ss(stream);
+  const uint64_t n_chunks = (total + width - 1) / width;
+  // Chunk j: bytes [j * width, ...) of the block, contiguous on the device,
+  // in one transfer to pinned half j % 2; the threads scatter chunk j - 1's
+  // units into their rows meanwhile.
+  for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
+    if (j < n_chunks) {
+      const uint64_t x0 = j * width, w = std::min(width, total - x0);
+      if (hipMemcpyAsync(h_pinned + (j % 2) * half, d_block + x0, w, hipMemcpyDeviceToHost,
+                         ss.st) != hipSuccess)
+        ss.fail();
+      ss.mark(j % 2);
+    }
+    if (j >= 1) {
+      const uint64_t p = j - 1, x0 = p * width, w = std::min(width, total - x0);
+      ss.wait(p % 2);
+      if (!ss.ok()) break;
+      ec::scatter_units(h_rows, positions, unit_bytes, x0, h_pinned + (p % 2) * half, w, threads);
+    }
+  }
+  if (!ss.ok()) (void)hipStreamSynchronize(ss.st);  // no transfer outlives the call
+  return ss.status;
 }
 
 int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row_bytes,
@@ -88,47 +161,30 @@ int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row
     if (!h_rows[r]) return EC_EINVAL;
   if (dst_pitch < row_bytes) return EC_EINVAL;
   const uint64_t half = pinned_bytes / 2;
-  uint64_t width = half / rows;
-  if (width >= 4096) width -= width % 4096;
+  uint64_t width = half_of(pinned_bytes, rows);
   if (width == 0) return EC_EINVAL;
   width = std::min(width, row_bytes);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  int prev = 0;
-  hipDevice_t sdev = 0;
-  if (hipGetDevice(&prev) != hipSuccess) return EC_EHIP;
-  if (st && hipStreamGetDevice(st, &sdev) != hipSuccess) return EC_EHIP;
-  const bool switched = st && sdev != prev;
-  if (switched && hipSetDevice(sdev) != hipSuccess) return EC_EHIP;
-  hipEvent_t ev[2] = {nullptr, nullptr};
-  int status = EC_OK;
-  for (auto& e : ev)
-    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
-      status = EC_EHIP;
+  Session ss(stream);
   const uint64_t n_chunks = (row_bytes + width - 1) / width;
   // Chunk j: the threads fill pinned half j % 2 (once the transfer of chunk
   // j - 2 out of it has landed), then the transfer is enqueued; the fill of
   // chunk j + 1 overlaps it.
-  for (uint64_t j = 0; status == EC_OK && j < n_chunks; ++j) {
+  for (uint64_t j = 0; ss.ok() && j < n_chunks; ++j) {
     const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
     uint8_t* pin = h_pinned + (j % 2) * half;
-    if (j >= 2 && hipEventSynchronize(ev[j % 2]) != hipSuccess) {
-      status = EC_EHIP;
-      break;
-    }
+    if (j >= 2) ss.wait(j % 2);
+    if (!ss.ok()) break;
     // rows x w bytes, split over the threads by equal shares of bytes
     ec::gather_rows(pin, h_rows, x0, rows, w, threads);
-    for (uint32_t r = 0; r < rows && status == EC_OK; ++r)
+    for (uint32_t r = 0; r < rows && ss.ok(); ++r)
       if (hipMemcpyAsync(d_dst + (uint64_t)r * dst_pitch + x0, pin + (uint64_t)r * w, w,
-                         hipMemcpyHostToDevice, st) != hipSuccess)
-        status = EC_EHIP;
-    if (status == EC_OK && hipEventRecord(ev[j % 2], st) != hipSuccess) status = EC_EHIP;
+                         hipMemcpyHostToDevice, ss.st) != hipSuccess)
+        ss.fail();
+    ss.mark(j % 2);
   }
   // no transfer outlives the call: the pinned buffer is the caller's again
-  if (hipStreamSynchronize(st) != hipSuccess && status == EC_OK) status = EC_EHIP;
-  for (auto& e : ev)
-    if (e) (void)hipEventDestroy(e);
-  if (switched) (void)hipSetDevice(prev);
-  return status;
+  if (hipStreamSynchronize(ss.st) != hipSuccess && ss.ok()) ss.fail();
+  return ss.status;
 }
 
 }  // extern "C"

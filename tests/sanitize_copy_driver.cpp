@@ -1,5 +1,6 @@
 // Host-side driver for the sanitizer test: the staging entry points' host
-// copies (ec::copy_rect, ec::gather_rows in megatron-lm_amd/csrc/host_copy.cpp)
+// copies (ec::copy_rect, ec::gather_rows, ec::scatter_units in
+// megatron-lm_amd/csrc/host_copy.cpp)
 // over odd pitches, widths, row counts and thread counts, against a plain
 // loop, under AddressSanitizer and UndefinedBehaviorSanitizer.  Buffers are
 // allocated to the exact extent each call may touch, so a read or write past
@@ -59,9 +60,48 @@ int main() {
               if (packed[r * width + x] != pattern(r + 9, x0 + x)) FAIL("gather_rows byte");
           ++cases;
         }
+  // scatter: a stripe-major (stripes, positions, unit) block, walked in
+  // chunks of every size class (within a unit, across units and stripes),
+  // into separately allocated position rows of exactly stripes * unit bytes
+  const uint32_t pos_list[] = {1, 3, 16};
+  const uint32_t stripe_list[] = {1, 2, 5};
+  const uint64_t unit_list[] = {1, 7, 64, 4099};
+  for (uint32_t positions : pos_list)
+    for (uint32_t stripes : stripe_list)
+      for (uint64_t unit : unit_list) {
+        const uint64_t total = (uint64_t)stripes * positions * unit;
+        std::vector<uint8_t> block(total);
+        for (uint64_t g = 0; g < total; ++g) block[g] = pattern(g / unit, g % unit);
+        const uint64_t chunk_list[] = {1, 13, unit, unit * positions + 5, total};
+        for (uint64_t chunk : chunk_list)
+          for (int threads : {1, 3, 8, 64}) {
+            if ((total + chunk - 1) / chunk > 300) continue;  // bounded thread start-ups
+            std::vector<std::vector<uint8_t>> rowbufs(positions);
+            std::vector<uint8_t*> ptrs(positions);
+            for (uint32_t p = 0; p < positions; ++p) {
+              rowbufs[p].assign(stripes * unit, 0xEE);
+              ptrs[p] = rowbufs[p].data();
+            }
+            for (uint64_t x0 = 0; x0 < total; x0 += chunk) {
+              const uint64_t len = chunk < total - x0 ? chunk : total - x0;
+              // the chunk as its own exact-size buffer, as a pinned half holds it
+              std::vector<uint8_t> piece(block.begin() + x0, block.begin() + x0 + len);
+              ec::scatter_units(ptrs.data(), positions, unit, x0, piece.data(), len, threads);
+            }
+            for (uint32_t p = 0; p < positions; ++p)
+              for (uint32_t st = 0; st < stripes; ++st)
+                for (uint64_t x = 0; x < unit; ++x)
+                  if (rowbufs[p][st * unit + x] != pattern((uint64_t)st * positions + p, x))
+                    FAIL("scatter_units positions %u stripes %u unit %lu chunk %lu threads %d: "
+                         "row %u stripe %u byte %lu", positions, stripes, (unsigned long)unit,
+                         (unsigned long)chunk, threads, p, st, (unsigned long)x);
+            ++cases;
+          }
+      }
   // zero rows or width: no access at all
   ec::copy_rect(nullptr, 0, nullptr, 0, 0, 16, 4);
   ec::gather_rows(nullptr, nullptr, 0, 3, 0, 4);
+  ec::scatter_units(nullptr, 3, 16, 0, nullptr, 0, 4);
   printf("sanitize copy driver ok: %d cases\n", cases);
   return 0;
 }

@@ -151,6 +151,26 @@ def test_stage_to_host_rejects_bad_arguments(pkg):
     assert L.ec_stage_to_host(p, 64, p, 64, 4, 64, p, 6, 4, None) == pkg._lib.EC_EINVAL
 
 
+def test_stage_stripes_to_host_rejects_bad_arguments(pkg):
+    """Host-side validation of ec_stage_stripes_to_host (no device work)."""
+    L = pkg._lib.lib()
+    p = ctypes.c_void_p(4096)
+    rows = (ctypes.c_void_p * 2)(4096, 8192)
+    hole = (ctypes.c_void_p * 2)(4096, None)
+    ok, bad = pkg._lib.EC_OK, pkg._lib.EC_EINVAL
+    assert L.ec_stage_stripes_to_host(p, 0, 2, 64, rows, p, 256, 4, None) == ok
+    assert L.ec_stage_stripes_to_host(p, 3, 0, 64, rows, p, 256, 4, None) == ok
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 0, rows, p, 256, 4, None) == ok
+    assert L.ec_stage_stripes_to_host(None, 3, 2, 64, rows, p, 256, 4, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, None, p, 256, 4, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, hole, p, 256, 4, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, rows, None, 256, 4, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, rows, p, 256, 0, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, rows, p, 256, 65, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 3, 2, 64, rows, p, 1, 4, None) == bad
+    assert L.ec_stage_stripes_to_host(p, 1 << 31, 2, 1 << 33, rows, p, 256, 4, None) == bad
+
+
 def test_stage_to_device_rejects_bad_arguments(pkg):
     """Host-side validation of ec_stage_to_device (no device work)."""
     L = pkg._lib.lib()

@@ -324,6 +324,59 @@ def test_batched_decode_stripe_subset(pkg, dev):
     assert lay.plan_decode(pset.parity, [1], stripes=[]) is None
 
 
+@pytest.mark.parametrize("k,m,unit,misalign,lost", [
+    ((6, 3, (2 << 20) + 1024, False, (0, 4, 7))),   # 2049 tiles a unit: spans not a multiple of 8
+    ((12, 4, (2 << 20) + 16, True, (1, 12))),       # realigned inputs, a 16-byte tail tile
+    ((8, 2, 4 << 20, True, (3, 9)))])
+def test_batched_sliced_order(pkg, dev, k, m, unit, misalign, lost):
+    """Units of 2 MiB and more are walked in 8 interleaved slices of the
+    grid (rounded up to whole slices; the workgroups past the last span do
+    nothing).  The encode equals the oracle's, the copying encode into a
+    stripe-major block writes the same parity and zero-padded copies, and
+    lost positions decode back."""
+    from megatron_lm_amd import _lib
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    rng = np.random.default_rng(unit + k)
+    host, tensors = _ragged_device(rng, dev, 7, 5 * unit, misalign)
+    lay = pkg.StripeLayout(tensors, k, m, unit)
+    par = lay.encode()
+    torch.cuda.synchronize()
+    want_par = _oracle_layout_parity(lay, host, unit)
+    assert np.array_equal(par.cpu().numpy(), want_par)
+    S = lay.n_stripes
+    block = torch.full((S, k + m, unit), 0xC3, dtype=torch.uint8, device=dev)
+    pp, cp = GpuSliceCodec._unit_ptrs(block, k, m), GpuSliceCodec._unit_ptrs(block, 0, k)
+    _lib.check(_lib.lib().ec_encode_batched_copy(
+        _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+        pp.data_ptr(), cp.data_ptr(), S, unit, None), "ec_encode_batched_copy")
+    torch.cuda.synchronize()
+    got = block.cpu().numpy()
+    del block
+    assert np.array_equal(got[:, k:], want_par)
+    for s in range(S):
+        for j in range(k):
+            u = s * k + j
+            want = np.zeros(unit, np.uint8)
+            if u < lay.n_units:
+                t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+                piece = host[t][i * unit: (i + 1) * unit]
+                want[: piece.size] = piece
+            assert np.array_equal(got[s, j], want), (s, j)
+    del got
+    for s in range(S):
+        for pos in lost:
+            u = s * k + pos
+            if pos < k and u < lay.n_units:
+                lay.unit_view(u).fill_(0xA5)
+            elif pos >= k:
+                par[s, pos - k].fill_(0x5A)
+    lay.decode(par, list(lost))
+    torch.cuda.synchronize()
+    for h, t in zip(host, tensors):
+        assert np.array_equal(t.cpu().numpy(), h)
+    assert np.array_equal(par.cpu().numpy(), want_par)
+
+
 @pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 2048, False), (6, 3, 20480, False),
                                                 (12, 4, 4096, True), (8, 2, 16384, True)])
 def test_batched_update_equals_reencode(pkg, dev, k, m, unit, misalign):
@@ -571,6 +624,35 @@ def test_stage_to_host(pkg, dev, rows, row_bytes, pitch, pinned, threads):
     want = src.cpu().numpy()
     assert np.array_equal(out[:, :row_bytes], want[:, :row_bytes])
     assert (out[:, row_bytes:] == 0x77).all()
+
+
+@pytest.mark.parametrize("stripes,positions,unit,pinned,threads", [
+    (300, 16, 4096 + 48, 1 << 20, 8),     # chunks end inside units, a short last one
+    (5, 3, 5000, 64, 1),                  # chunks narrower than a unit and a page
+    (40, 10, 1 << 16, 64 << 20, 64),      # one chunk for the whole block
+    (2, 1, 7, 4096, 3),                   # one position: a plain copy
+])
+def test_stage_stripes_to_host(pkg, dev, stripes, positions, unit, pinned, threads):
+    """ec_stage_stripes_to_host moves a stripe-major (stripes, positions,
+    unit) device block into one pageable host row per position, exactly:
+    row p is unit (s, p) for s = 0, 1, ..., back to back, and nothing past
+    a row's end is written.  The copy follows the work already on the
+    stream."""
+    from megatron_lm_amd import _lib
+    g = torch.Generator(device=dev)
+    g.manual_seed(stripes)
+    block = torch.randint(0, 256, (stripes, positions, unit), dtype=torch.uint8, device=dev,
+                          generator=g)
+    rows = [np.full(stripes * unit + 16, 0x77, np.uint8) for _ in range(positions)]
+    pin = torch.empty(pinned, dtype=torch.uint8, pin_memory=True)
+    block.add_(1)   # enqueued before the call: the copy must see it
+    _lib.check(_lib.lib().ec_stage_stripes_to_host(
+        block.data_ptr(), stripes, positions, unit, _lib.ptr_array([r.ctypes.data for r in rows]),
+        pin.data_ptr(), pinned, threads, None), "ec_stage_stripes_to_host")
+    want = block.cpu().numpy()
+    for p in range(positions):
+        assert np.array_equal(rows[p][:stripes * unit], want[:, p, :].reshape(-1)), p
+        assert (rows[p][stripes * unit:] == 0x77).all(), p
 
 
 @pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [

@@ -112,14 +112,15 @@ def test_placement(g, k, m, jump):
             assert len({s.holder(owner, p) // jump for p in range(k + m)}) == k + m
 
 
-def test_row_addresses_on_device_match_host():
-    """The snapshot's device-computed unit addresses equal the host ones."""
+def test_unit_addresses_on_device_match_the_block():
+    """The snapshot's device-computed unit addresses are those of the units
+    of its stripe-major (stripes, positions, unit_bytes) block."""
     import torch
-    block = torch.empty((7, 5, 48), dtype=torch.uint8)
+    block = torch.empty((5, 7, 48), dtype=torch.uint8)
     for first, count in ((0, 4), (4, 3), (2, 1)):
-        want = np.stack([ck.GpuSliceCodec._rows(block, p) for p in range(first, first + count)],
-                        axis=1).view(np.int64)
-        got = ck.GpuSliceCodec._row_ptrs(block, first, count).numpy()
+        want = np.array([[block[s, p].data_ptr() for p in range(first, first + count)]
+                         for s in range(5)], dtype=np.int64)
+        got = ck.GpuSliceCodec._unit_ptrs(block, first, count).numpy()
         assert np.array_equal(got, want), (first, count)
 
 
