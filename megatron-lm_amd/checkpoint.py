@@ -58,7 +58,6 @@ import re
 import threading
 import time
 import weakref
-from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Callable, Dict, List, NamedTuple, Optional, Sequence, Tuple
@@ -223,7 +222,7 @@ class GpuSliceCodec:
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.chunk_bytes = chunk_bytes
         self.snapshot_bytes = snapshot_bytes
-        self.stage_threads = 8   # host threads of a snapshot's background staging
+        self.stage_threads = 8   # host threads of the staging calls
         self._free: Optional[np.ndarray] = None   # released by the caller, reusable
         self._host_lock = threading.Lock()
 
@@ -294,53 +293,6 @@ class GpuSliceCodec:
                 "n_stripes": lay.n_stripes, "n_units": lay.n_units,
                 "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
 
-    def _to_host(self, rows: int, chunks, C: int, src, out: np.ndarray, copy, pool,
-                 produce=None) -> None:
-        """Move chunk n = (first stripe, stripes) of a device (rows, stripes,
-        unit_bytes) source into the host array ``out`` (rows, S * unit_bytes)
-        through two pinned (rows, C, unit_bytes) buffers: transfers on the
-        ``copy`` stream, row by row (a row's part of a chunk is contiguous),
-        then copied into ``out`` by the pool's threads while the next chunk
-        is in flight.  ``src(n)`` is chunk n's device view;
-        ``produce(n, landed)``, when given, enqueues what fills it and makes
-        ``copy`` wait for that (``landed[j]`` = chunk j has reached pinned
-        memory)."""
-        U, nb = self.unit_bytes, min(2, len(chunks))
-        pins = [torch.empty((rows, C, U), dtype=torch.uint8, pin_memory=True)
-                for _ in range(nb)]
-        landed: List[torch.cuda.Event] = []
-        drained: List[list] = []   # host copies of chunk n out of pins[n % nb]
-
-        def drain(n):
-            c0, c = chunks[n]
-            landed[n].synchronize()
-            pinned = pins[n % nb].numpy()[:, :c].reshape(rows, -1)
-            return _copy_rows(pool, out[:, c0 * U:(c0 + c) * U], lambda r: pinned[r])
-
-        for n, (c0, c) in enumerate(chunks):
-            b = n % nb
-            if produce is not None:
-                produce(n, landed)
-            if n >= nb:
-                for f in drained[n - nb]:   # pinned buffer b is free again
-                    f.result()
-            view = src(n)
-            with torch.cuda.stream(copy):
-                for r in range(rows):
-                    pins[b][r, :c].copy_(view[r], non_blocking=True)
-            landed.append(torch.cuda.Event())
-            landed[-1].record(copy)
-            if n >= 1:
-                drained.append(drain(n - 1))   # overlaps chunk n's transfer
-        drained.append(drain(len(chunks) - 1))
-        for fs in drained[-nb:]:
-            for f in fs:
-                f.result()
-
-    @staticmethod
-    def _pool() -> ThreadPoolExecutor:
-        return ThreadPoolExecutor(max_workers=_COPY_THREADS)
-
     def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         """Code the tensors into k + m slices in host memory; returns when
         they are there.  Through one HBM block when it fits (``snapshot``,
@@ -348,10 +300,13 @@ class GpuSliceCodec:
         return self.snapshot(tensors).result()
 
     def _encode_chunked(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
-        """Code and stage in bounded chunks; returns when the slices are in
-        host memory.  The kernels run on torch's current stream (ordered after
-        the work that produced the tensors), the transfers on a stream of
-        torch's pool."""
+        """Code and stage in bounded chunks of stripes; returns when the slices
+        are in host memory.  Each chunk is one copying-encode launch on torch's
+        current stream (ordered after the work that produced the tensors) into
+        a stripe-major (stripes, k + m, unit_bytes) device buffer, which
+        ``ec_stage_stripes_to_host`` then moves into the slice rows on an
+        ordinary stream.  Two buffers alternate: chunk n + 1 is coded while
+        chunk n is staged."""
         from . import _lib
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
@@ -362,35 +317,41 @@ class GpuSliceCodec:
         chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
         nb = min(2, len(chunks))
         out = self._host_out((k + m, S * U))
-        with torch.cuda.device(dev), self._pool() as pool:
+        rows = [out[p].ctypes.data for p in range(k + m)]
+        with torch.cuda.device(dev):
             # transfers on an ordinary stream (on the CU-masked side stream they
             # held the host and slowed the kernels beside them)
-            comp, copy = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
-            bufs = [torch.empty((k + m, C, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
-            # per buffer: parity unit (s, i) -> row k + i, data unit (s, p) -> row p
-            pp = [self._dev(np.stack([self._rows(b, k + i) for i in range(m)], axis=1), np.int64,
-                            dev) for b in bufs]
-            gp = [self._dev(np.stack([self._rows(b, p) for p in range(k)], axis=1), np.int64, dev)
-                  for b in bufs]
+            comp, xfer = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
+            bufs = [torch.empty((C, k + m, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
+            pp = [self._unit_ptrs(b, k, m) for b in bufs]
+            gp = [self._unit_ptrs(b, 0, k) for b in bufs]
             for b in bufs:
-                b.record_stream(copy)
+                b.record_stream(xfer)
+            pinned = torch.empty(min(2 * self.chunk_bytes, 2 * C * (k + m) * U),
+                                 dtype=torch.uint8, pin_memory=True)
 
-            def produce(n, landed):
+            def code(n):
                 c0, c = chunks[n]
                 b = n % nb
-                if n >= nb:
-                    comp.wait_event(landed[n - nb])    # device buffer b is free again
-                dp = lay.d_ptrs.data_ptr() + c0 * k * 8
-                dl = lay.d_len.data_ptr() + c0 * k * 4
                 _lib.check(_lib.lib().ec_encode_batched_copy(
-                    _lib.u8ptr(lay.coeff), k, m, dp, dl, pp[b].data_ptr(), gp[b].data_ptr(), c,
+                    _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr() + c0 * k * 8,
+                    lay.d_len.data_ptr() + c0 * k * 4, pp[b].data_ptr(), gp[b].data_ptr(), c,
                     U, stream_handle(comp, dev)), "ec_encode_batched_copy")
                 ready = torch.cuda.Event()
                 ready.record(comp)
-                copy.wait_event(ready)
+                return ready
 
-            self._to_host(k + m, chunks, C, lambda n: bufs[n % nb][:, :chunks[n][1]], out,
-                          copy, pool, produce)
+            ready = code(0)
+            for n, (c0, c) in enumerate(chunks):
+                xfer.wait_event(ready)
+                # the other buffer's last chunk (n - 1) was staged by the call
+                # before, which returned once its bytes were in host memory
+                ready = code(n + 1) if n + 1 < len(chunks) else None
+                _lib.check(_lib.lib().ec_stage_stripes_to_host(
+                    bufs[n % nb].data_ptr(), c, k + m, U,
+                    _lib.ptr_array([r + c0 * U for r in rows]), pinned.data_ptr(),
+                    pinned.numel(), self.stage_threads, stream_handle(xfer, dev)),
+                    "ec_stage_stripes_to_host")
         return self._meta(lay, tensors), [out[p] for p in range(k + m)]
 
     def snapshot(self, tensors: Sequence[torch.Tensor], hold: bool = True) -> "PendingSlices":
@@ -1154,23 +1115,6 @@ class ECLocalCheckpointManager:
             state.insert_tensors(tensors)
             return state, self._ckpt_id(it)
         return TensorListState(tensors, meta.get("common", {})), self._ckpt_id(it)
-
-
-_COPY_THREADS = 16   # the box's CPU share per GPU
-
-
-def _copy_rows(pool: ThreadPoolExecutor, dst: np.ndarray, src_row: Callable) -> list:
-    """dst[r] <- src_row(r) for the rows of a 2-D host array, split over the
-    pool's threads (numpy drops the GIL while it copies).  For the blocking
-    paths, whose caller waits anyway; a snapshot's background staging runs in
-    ec_stage_to_host instead.  Returns the futures."""
-    groups = np.array_split(np.arange(dst.shape[0]), min(_COPY_THREADS, dst.shape[0]))
-
-    def run(rows):
-        for r in rows:
-            np.copyto(dst[r], src_row(int(r)))
-
-    return [pool.submit(run, g) for g in groups if g.size]
 
 
 def _common(state) -> dict:

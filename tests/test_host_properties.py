@@ -124,20 +124,6 @@ def test_unit_addresses_on_device_match_the_block():
         assert np.array_equal(got, want), (first, count)
 
 
-def test_copy_rows_over_a_pool():
-    """The blocking paths' host copies: every row lands whole, whatever the
-    row count against the pool's threads."""
-    from concurrent.futures import ThreadPoolExecutor
-    rng = np.random.default_rng(3)
-    with ThreadPoolExecutor(max_workers=4) as pool:
-        for rows in (1, 3, 16, 17):
-            src = rng.integers(0, 256, (rows, 1000), dtype=np.uint8)
-            dst = np.zeros((rows, 1000), np.uint8)
-            for f in ck._copy_rows(pool, dst, lambda r: src[r]):
-                f.result()
-            assert np.array_equal(dst, src), rows
-
-
 def test_await_marker(tmp_path):
     """async_fn of a background save: returns once the marker exists, raises
     TimeoutError when it never comes."""
