@@ -9,9 +9,11 @@ namespace ec {
 namespace {
 
 // ------------------------------------------------ batched stripe kernels --
-// Grid = n_stripes x tiles_per_unit workgroups, stripe-major, so consecutive
-// workgroups stream adjacent bytes of the same k units.  The descriptor of a
-// stripe is uniform across the workgroup (scalar loads).
+// One workgroup per span of tiles (n_stripes x blocks_per_unit spans),
+// stripe-major: in launch order consecutive workgroups stream adjacent bytes
+// of the same k units; units of kSliceMinUnit and more are dealt in kSlices
+// interleaved slices instead (below).  The descriptor of a stripe is uniform
+// across the workgroup (scalar loads).
 //
 // The product launches one-wavefront workgroups with one 16-byte chunk per
 // lane, one 1 KiB tile of one stripe per workgroup (kBatchBlock, U = 1).
@@ -40,7 +42,7 @@ struct BatchArgs {
   uint32_t tiles_per_unit;   // tiles of B*U*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
-  uint32_t n_spans;          // n_stripes * blocks_per_unit: the real workgroups
+  uint32_t n_spans;          // n_stripes * blocks_per_unit: the spans to code
   uint32_t slices;           // the grid's interleaved slices (1: launch order)
   uint32_t slice_spans;      // ceil(n_spans / slices)
 };
