@@ -12,7 +12,7 @@ namespace {
 // One workgroup per span of tiles (n_stripes x blocks_per_unit spans),
 // stripe-major: in launch order consecutive workgroups stream adjacent bytes
 // of the same k units; units of kSliceMinUnit and more are dealt in kSlices
-// interleaved slices instead (below).  The descriptor of a stripe is uniform
+// interleaved slices instead (SpanGrid).  The descriptor of a stripe is uniform
 // across the workgroup (scalar loads).
 //
 // The product launches one-wavefront workgroups with one 16-byte chunk per
@@ -42,25 +42,8 @@ struct BatchArgs {
   uint32_t tiles_per_unit;   // tiles of B*U*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
-  uint32_t n_spans;          // n_stripes * blocks_per_unit: the spans to code
-  uint32_t slices;           // the grid's interleaved slices (1: launch order)
-  uint32_t slice_spans;      // ceil(n_spans / slices)
+  SpanGrid grid;             // n_stripes * blocks_per_unit spans
 };
-
-// Units of at least this size are walked in kSlices interleaved slices.
-// Workgroups are dispatched round-robin over the 8 XCDs, so with 8 slices
-// workgroup b takes span (b % 8) * slice_spans + b / 8: each XCD streams its
-// own eighth of the stripes, and the work in flight sits at 8 unrelated
-// offsets of the units instead of one.  With large units the k units a
-// workgroup reads lie a unit apart, and in launch order every workgroup in
-// flight reads the same few offsets of them.  Measured on MI355X (RS(8,2)
-// encode over 20.8 GB, fraction of the 8 TB/s roofline, launch order ->
-// 8 slices): 2 MiB units 0.741 -> 0.750, 4 MiB 0.723 -> 0.736, 8 MiB 0.691
-// -> 0.736, 16 MiB 0.584 -> 0.700, 32 MiB 0.621 -> 0.720, 64 MiB 0.685 ->
-// 0.724; below 2 MiB the slices cost 2-5 % (1 MiB 0.776 -> 0.734), and
-// 64 KiB units gained nothing.
-constexpr uint32_t kSliceMinUnit = 2u << 20;
-constexpr uint32_t kSlices = 8;
 
 // Zeros in device memory, read-only: on the fast path a unit that ended
 // before the current tile is read from here instead of branching, so the
@@ -195,10 +178,8 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   // The span this workgroup takes (uniform: a scalar branch); the grid is
   // rounded up to whole slices, and the few workgroups past the last span
   // return before any work.
-  const uint32_t b = a.slices == 1
-                         ? blockIdx.x
-                         : (blockIdx.x % a.slices) * a.slice_spans + blockIdx.x / a.slices;
-  if (b >= a.n_spans) return;
+  const uint32_t b = span_of(a.grid);
+  if (b >= a.grid.n_spans) return;
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
   // Workgroup b covers tiles [t0, t1) of one stripe: the descriptor loads and
@@ -287,12 +268,9 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
-  const uint64_t spans = (uint64_t)n_stripes * a.blocks_per_unit;
-  a.slices = unit_bytes >= kSliceMinUnit ? kSlices : 1u;
-  if (spans + a.slices - 1 > 0x7fffffffull) return EC_ERANGE;
-  a.n_spans = (uint32_t)spans;
-  a.slice_spans = (uint32_t)((spans + a.slices - 1) / a.slices);
-  const uint64_t blocks = (uint64_t)a.slice_spans * a.slices;
+  const uint64_t blocks = span_grid(a.grid, (uint64_t)n_stripes * a.blocks_per_unit,
+                                    slices_for(unit_bytes));
+  if (blocks == 0) return EC_ERANGE;
   hipLaunchKernelGGL((batched_kernel<K, M, U, COPY, B>), dim3((unsigned)blocks), dim3(B), 0,
                      st, a);
   return hip_status();

@@ -355,7 +355,11 @@ int launch_batched_wide_b(const uint8_t* coeff, int k, const uint64_t* dptr, con
 
 // Encode and decode with m <= 4 run one-wavefront workgroups on one 1 KiB
 // tile each, like the fixed-size batched kernel; wider outputs and the update
-// keep 256-lane workgroups.  Measured on MI355X (HBM traffic, GB/s, 8 GiB
+// keep 256-lane workgroups.  Both keep launch order for every unit size:
+// the fixed-size kernel's 8 slices for large units (SpanGrid) gained nothing
+// here and cost RS(16,6) over 4 MiB units 11 % (encode 0.606 -> 0.539 of the
+// roofline; RS(20,4) 4 MiB 0.661 -> 0.659, RS(24,8) 2 MiB 0.498 -> 0.496;
+// the 1 % update of RS(12,4) and RS(8,2) over 4 MiB units within 1 %).  Measured on MI355X (HBM traffic, GB/s, 8 GiB
 // buffers): RS(20,4) over 4 MiB units encode 5041 -> 5314, decode of 4
 // positions 4886 -> 5136; with m >= 6 the per-workgroup table build (m * k
 // tables) made one-wavefront workgroups 5 % slower (RS(16,6) over 64 KiB
