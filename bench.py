@@ -600,8 +600,8 @@ def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
     """Counter-run workload for the batched launcher, three launches each, in
     this order: the engine's streaming copy of one 256 MiB shard (the
     calibration kernel of known traffic); config 5 (RS(12,4), 3,000 ragged
-    tensors, 64 KiB units): encode, copying encode into one (16, stripes,
-    64 KiB) block (the snapshot's kernel), decode of lost positions 1, 7, 12,
+    tensors, 64 KiB units): encode, copying encode into one stripe-major
+    (stripes, 16, 64 KiB) block (the snapshot's kernel), decode of lost positions 1, 7, 12,
     14, 1 % update; config 4 (RS(8,2), 20.8 GB buffer, 4 MiB units) encode.
     Prints the launch groups with their algorithmic bytes as JSON."""
     import numpy as np

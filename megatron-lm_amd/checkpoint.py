@@ -225,6 +225,20 @@ class GpuSliceCodec:
         self.stage_threads = 8   # host threads of the staging calls
         self._free: Optional[np.ndarray] = None   # released by the caller, reusable
         self._host_lock = threading.Lock()
+        self._last_layout = None   # descriptors of the last encode, without its tensors
+        self._last_ptrs = None     # (block key, parity table, data table) of the last snapshot
+
+    def _stripe_layout(self, tensors: List[torch.Tensor]):
+        """The StripeLayout of the tensors to encode.  When they occupy the
+        same device bytes as at the last encode (a training run saves the
+        same buffers every time), its descriptors are reused: no descriptor
+        build and no upload on the path that holds training."""
+        prev = self._last_layout
+        lay = prev.rebind(tensors) if prev is not None else None
+        if lay is None:
+            lay = self._layout.StripeLayout(tensors, self.k, self.m, self.unit_bytes)
+            self._last_layout = lay.descriptors_only()
+        return lay
 
     def _host_out(self, shape: Tuple[int, int]) -> np.ndarray:
         """The released host array when it has this shape, else a new one.
@@ -261,6 +275,21 @@ class GpuSliceCodec:
         unit_bytes) device block."""
         S, U = block.shape[1], block.shape[2]
         return np.uint64(block[p].data_ptr()) + np.arange(S, dtype=np.uint64) * np.uint64(U)
+
+    def _block_ptrs(self, block: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(parity, data) unit-address tables of a snapshot block.  They
+        depend only on the block's address and shape, and the caching
+        allocator usually hands the same block back at the next save, so the
+        last pair is kept and reused when it matches."""
+        key = (block.device, block.data_ptr(), tuple(block.shape))
+        last = self._last_ptrs
+        if last is not None and last[0] == key:
+            return last[1], last[2]
+        with torch.cuda.device(block.device):
+            pp = self._unit_ptrs(block, self.k, self.m)
+            gp = self._unit_ptrs(block, 0, self.k)
+        self._last_ptrs = (key, pp, gp)
+        return pp, gp
 
     @staticmethod
     def _unit_ptrs(block: torch.Tensor, first: int, count: int) -> torch.Tensor:
@@ -311,7 +340,7 @@ class GpuSliceCodec:
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
-        lay = self._layout.StripeLayout(tensors, k, m, U)
+        lay = self._stripe_layout(tensors)
         S, dev = lay.n_stripes, lay.device
         C = self._chunk_stripes(S, k + m)
         chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
@@ -383,7 +412,7 @@ class GpuSliceCodec:
         from .codec import side_stream, stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
-        lay = self._layout.StripeLayout(tensors, k, m, U)
+        lay = self._stripe_layout(tensors)
         S, dev = lay.n_stripes, lay.device
         cur = torch.cuda.current_stream(dev)
         block = None
@@ -399,9 +428,7 @@ class GpuSliceCodec:
             coded.record(cur)
             return PendingSlices(coded, ready=ready)
         side = side_stream(dev)
-        with torch.cuda.device(dev):
-            pp = self._unit_ptrs(block, k, m)
-            gp = self._unit_ptrs(block, 0, k)
+        pp, gp = self._block_ptrs(block)
         for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
             t.record_stream(side)
         side.wait_stream(cur)   # the tensors' producers and the descriptor uploads

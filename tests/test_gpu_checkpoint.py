@@ -206,3 +206,49 @@ def test_gpu_side_stream_use_outlives_exit_hooks(dev):
     r = subprocess.run([sys.executable, "-c", code, ROOT], capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 0 and "enqueued" in r.stdout, (r.returncode, r.stderr[-2000:])
+
+
+def test_gpu_encode_reuses_descriptors_of_the_same_buffers(dev):
+    """A save of tensors occupying the same device bytes as the last one
+    reuses its stripe descriptors; another address, a shorter tensor, another
+    order or a changed value in place all give the right slices (the first
+    three through fresh descriptors), and the kept descriptors hold no
+    reference to the tensors."""
+    import weakref
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    k, m, unit = 4, 2, 1024
+    cpu = make_tensors(3) + make_tensors(2)
+    gpu = [t.to(dev) for t in cpu]
+    codec = GpuSliceCodec(k, m, unit)
+    oracle = OracleSliceCodec(k, m, unit)
+
+    def check(gt, ct):
+        meta, sl = codec.encode(gt)
+        assert meta == oracle.encode(ct)[0]
+        for p, (a, b) in enumerate(zip(sl, oracle.encode(ct)[1])):
+            assert np.array_equal(a, b), f"slice {p}"
+        codec.release(sl)
+
+    check(gpu, cpu)
+    kept = codec._last_layout
+    assert kept.tensors == []
+    bump(gpu[1])                             # same bytes, new values: reused
+    cpu[1] = gpu[1].cpu()
+    check(gpu, cpu)
+    assert codec._last_layout is kept
+    moved = list(gpu)
+    moved[2] = gpu[2].clone()                # another address
+    check(moved, cpu)
+    assert codec._last_layout is not kept
+    kept = codec._last_layout
+    short = list(moved)
+    short[0] = moved[0].reshape(-1)[:-3]     # the same address, fewer bytes
+    check(short, [cpu[0].reshape(-1)[:-3]] + cpu[1:])
+    assert codec._last_layout is not kept
+    swapped = [moved[1], moved[0]] + moved[2:]
+    check(swapped, [cpu[1], cpu[0]] + cpu[2:])
+    probe = weakref.ref(swapped[3])
+    del gpu, moved, short, swapped
+    import gc
+    gc.collect()
+    assert probe() is None
