@@ -466,9 +466,11 @@ def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
     GpuSliceCodec.snapshot codes them into one HBM block on the side stream
     and holds torch's stream only until that is done (the stall a save costs
     training), then stages the block to host memory in a background thread
-    while GEMMs run on torch's stream.  Reports the stall, the staging time to
-    host memory, and the GEMM time per call during the staging next to its
-    time alone; the slices are checked against the synchronous encode's."""
+    while GEMMs run on torch's stream.  Reports the stall (median of three
+    saves, each right after 20 GEMMs have run, as a save follows a training
+    step), the staging time to host memory, and the GEMM time per call during
+    the last save's staging next to its time alone; the slices are checked
+    against the synchronous encode's."""
     import numpy as np
     import torch
     from megatron_lm_amd.checkpoint import GpuSliceCodec
@@ -477,13 +479,18 @@ def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
     try:
         g_alone = gemm.ms_alone()
         codec.release(codec.snapshot(tensors).result()[1])   # warm: pinned buffers, host array
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        pending = codec.snapshot(tensors)
-        mark = torch.cuda.Event()
-        mark.record()                 # torch's stream passes it once the coding is done
-        mark.synchronize()
-        t_stall = time.perf_counter() - t0
+        stalls = []
+        for rep in range(3):
+            gemm.enqueue(20)[1].synchronize()   # a training step's GPU work has just ended
+            t0 = time.perf_counter()
+            pending = codec.snapshot(tensors)
+            mark = torch.cuda.Event()
+            mark.record()             # torch's stream passes it once the coding is done
+            mark.synchronize()
+            stalls.append(time.perf_counter() - t0)
+            if rep < 2:
+                codec.release(pending.result()[1])
+        t_stall = sorted(stalls)[1]
         # about 0.25 s of GEMMs, enqueued at once so that no host gap enters
         # their timing, inside the staging (which takes about twice as long)
         n_gemm = max(10, int(0.25 / (g_alone * 1e-3)))
@@ -503,6 +510,7 @@ def checkpoint_snapshot(pkg, tensors, gemm: "GemmLoad") -> dict:
         codec.release(slices)
         del again, slices
         res = {"ckpt_snapshot_stall_ms": round(t_stall * 1e3, 2),
+               "ckpt_snapshot_stall_ms_each": [round(x * 1e3, 2) for x in stalls],
                "ckpt_snapshot_stall_data_GBps": round(nbytes / t_stall / 1e9, 1),
                "ckpt_snapshot_staged_s": round(t_staged, 3),
                "ckpt_snapshot_gemm_ms_alone": round(g_alone, 3),
