@@ -859,11 +859,14 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true",
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
-    ap.add_argument("--mode", choices=["full", "headline", "decode", "pmc", "batched",
-                                       "batched-kernels", "batched-pmc", "gf-variants", "train"],
+    ap.add_argument("--mode", choices=["full", "headline", "decode", "flat-kernels", "pmc",
+                                       "batched", "batched-kernels", "batched-pmc",
+                                       "gf-variants", "train"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
-                         "encode (for kernel-trace profiles); pmc: a few launches of a "
+                         "encode (for kernel-trace profiles); flat-kernels: configs 2, 3 "
+                         "and 1 and the streaming-copy ceiling, timed as in full (for "
+                         "kernel-trace profiles); pmc: a few launches of a "
                          "plain 256 MiB copy and of the RS(6,3) encode, for counter runs; "
                          "batched: configs 4 and 5 only; batched-kernels: the same without "
                          "the checkpoint staging and snapshot (for kernel-trace profiles); "
@@ -964,6 +967,18 @@ def main() -> int:
         raise AssertionError("XOR parity does not reproduce the shards")
     xor_gbs = 4 * 64 * MiB / (xwall * 1e-3) / 1e9
     log(f"XOR(4) {xor_gbs:.1f} GB/s data")
+    if args.mode == "flat-kernels":
+        del xd, xp, back
+        src = torch.empty(k * shard, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        _, cev = timed(lambda: pkg.xor_encode([src], out=dst), 50, 10)
+        print(json.dumps({"mode": "flat-kernels", "encode_GBps": round(enc_gbs, 2),
+                          "encode_kernel_us": round(ev_ms * 1e3, 2),
+                          "decode_GBps": round(dec_gbs, 2), "decode_kernel_us": round(dev_ms * 1e3, 2),
+                          "xor_GBps": round(xor_gbs, 2), "xor_kernel_us": round(xev * 1e3, 2),
+                          "copy_kernel_us": round(cev * 1e3, 2),
+                          "copy_GBps": round(2 * src.numel() / (cev * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
     small = small_shards(pkg, dev)
 
     gemm = GemmLoad(dev)
