@@ -563,9 +563,11 @@ def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
 
 def small_shards(pkg, dev) -> dict:
     """RS(6,3) over small shards, where the per-call host work competes with
-    the kernel: back-to-back calls through matvec (checks and ctypes arrays
-    built on every call) and through a ShardPlan (built once, one foreign
-    call per launch).  HBM traffic GB/s over wall time, 9 shards per call."""
+    the kernel: back-to-back eager calls (matvec into given outputs, and
+    rs_encode allocating its parity; each checks its tensors in the torch
+    binding on every call) and launches of a ShardPlan (built once, one
+    foreign call per launch).  HBM traffic GB/s over wall time, 9 shards per
+    call."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(3)
@@ -579,10 +581,13 @@ def small_shards(pkg, dev) -> dict:
         plan = pkg.ShardPlan(coeff, data, out=par)
         calls = 400
         w_eager, _ = timed(lambda: pkg.matvec(coeff, data, out=par), calls, 50)
+        w_alloc, _ = timed(lambda: pkg.rs_encode(data, 3), calls, 50)
         w_plan, _ = timed(plan, calls, 50)
         out[f"rs63_{mib}MiB_eager_traffic_GBps"] = round(9 * n / (w_eager * 1e-3) / 1e9, 1)
+        out[f"rs63_{mib}MiB_eager_alloc_traffic_GBps"] = round(9 * n / (w_alloc * 1e-3) / 1e9, 1)
         out[f"rs63_{mib}MiB_plan_traffic_GBps"] = round(9 * n / (w_plan * 1e-3) / 1e9, 1)
         out[f"rs63_{mib}MiB_eager_us_per_call"] = round(w_eager * 1e3, 2)
+        out[f"rs63_{mib}MiB_eager_alloc_us_per_call"] = round(w_alloc * 1e3, 2)
         out[f"rs63_{mib}MiB_plan_us_per_call"] = round(w_plan * 1e3, 2)
     log(f"small shards: {out}")
     return out
@@ -861,7 +866,7 @@ def main() -> int:
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
     ap.add_argument("--mode", choices=["full", "headline", "decode", "flat-kernels", "pmc",
                                        "batched", "batched-kernels", "batched-pmc",
-                                       "gf-variants", "train"],
+                                       "gf-variants", "train", "small-shards"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); flat-kernels: configs 2, 3 "
@@ -873,7 +878,8 @@ def main() -> int:
                          "batched-pmc: the copy plus 3 launches of each batched kernel, for "
                          "counter runs; gf-variants: "
                          "the v_perm GF multiply against LDS log/exp tables; train: a training "
-                         "loop with synchronous and with snapshot checkpoint saves")
+                         "loop with synchronous and with snapshot checkpoint saves; "
+                         "small-shards: RS(6,3) over 1 and 4 MiB shards, eager and planned")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the erasure-coding path has no multi-GPU "
@@ -901,6 +907,9 @@ def main() -> int:
         return batched_pmc_launches(pkg, synth, dev, args.seed)
     if args.mode == "gf-variants":
         return gf_variants(pkg, synth, dev, args.seed, min(args.steps, 50))
+    if args.mode == "small-shards":
+        print(json.dumps({"mode": args.mode, **small_shards(pkg, dev)}), flush=True)
+        return 0
     if args.mode == "train":
         print(json.dumps({"mode": "train", **training_with_checkpoints(pkg, dev)}), flush=True)
         return 0

@@ -2,7 +2,8 @@
 
 The shared library is built in-tree by ``__graft_entry__.build()``.  There is
 no fallback: if the library is missing, every call raises
-``ECLibraryMissing``.
+``ECLibraryMissing``.  ``shards()`` loads the torch-tensor binding of the
+flat-shard calls, built beside it.
 """
 from __future__ import annotations
 
@@ -119,6 +120,33 @@ def lib() -> ctypes.CDLL:
     L.ec_stage_to_device.argtypes = [_vp, _u32, _u64, _vp, _u64, _vp, _u64, _i, _vp]
     _lib = L
     return L
+
+
+SHARDS_NAME = "_ec_shards"
+SHARDS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), SHARDS_NAME + ".so")
+_shards_mod = None
+
+
+def shards():
+    """The torch-tensor binding of the flat-shard calls (``_ec_shards.so``,
+    csrc/shards_torch.cpp), which links libec_mi355.so.  Raises
+    ``ECLibraryMissing`` when it is not built; there is no fallback."""
+    global _shards_mod
+    if _shards_mod is not None:
+        return _shards_mod
+    lib()  # the C library first: checks its ABI version and gives the extension its symbols
+    if not os.path.exists(SHARDS_PATH):
+        raise ECLibraryMissing(
+            f"{SHARDS_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    import importlib.machinery
+    import importlib.util
+    import torch  # noqa: F401  (the extension needs torch's libraries loaded)
+    loader = importlib.machinery.ExtensionFileLoader(SHARDS_NAME, SHARDS_PATH)
+    spec = importlib.util.spec_from_file_location(SHARDS_NAME, SHARDS_PATH, loader=loader)
+    mod = importlib.util.module_from_spec(spec)
+    loader.exec_module(mod)
+    _shards_mod = mod
+    return mod
 
 
 def strerror(status: int) -> str:

@@ -43,13 +43,19 @@ def stream_handle(stream: Optional[torch.cuda.Stream] = None,
     ``device`` (torch's current device if None).  The kernels run on the
     stream's device, so a stream on another device than the data is
     rejected."""
+    return ctypes.c_void_p(_raw_stream(stream, device))
+
+
+def _raw_stream(stream, device) -> int:
+    """The raw handle behind ``stream_handle``, as an int."""
     if stream is None:
-        s = torch.cuda.current_stream(device)
-    else:
-        s = stream
-        if device is not None and s.device != torch.device(device):
-            raise ValueError(f"stream is on {s.device}, the tensors on {device}")
-    return ctypes.c_void_p(s.cuda_stream)
+        if device is None:
+            return _lib.shards().current_stream(-1)
+        dev = torch.device(device)
+        return _lib.shards().current_stream(-1 if dev.index is None else dev.index)
+    if device is not None and stream.device != torch.device(device):
+        raise ValueError(f"stream is on {stream.device}, the tensors on {device}")
+    return stream.cuda_stream
 
 
 _side: Dict[Tuple[int, int], torch.cuda.ExternalStream] = {}
@@ -121,6 +127,17 @@ def cauchy_matrix(k: int, m: int) -> np.ndarray:
     return out
 
 
+_cauchy_bytes: Dict[Tuple[int, int], bytes] = {}
+
+
+def _cauchy_cached(k: int, m: int) -> bytes:
+    """cauchy_matrix(k, m) as bytes, computed once per (k, m)."""
+    b = _cauchy_bytes.get((k, m))
+    if b is None:
+        b = _cauchy_bytes.setdefault((k, m), cauchy_matrix(k, m).tobytes())
+    return b
+
+
 def gf_invert(a: np.ndarray) -> np.ndarray:
     a = np.ascontiguousarray(a, np.uint8)
     n = a.shape[0]
@@ -170,32 +187,41 @@ def _outputs(out, n: int, nbytes: int, device, what: str) -> List[torch.Tensor]:
     return out
 
 
+# The eager calls below go through the torch-tensor binding (_lib.shards()):
+# it checks the tensors, allocates missing outputs, finds torch's current
+# stream and makes the C call in one crossing from Python.
+
+def _shard_call(op: int, coeff: bytes, m: int, shards, out, stream, what: str):
+    if len(shards) == 0:
+        raise ValueError("no shards")
+    raw = None if stream is None else _raw_stream(stream, getattr(shards[0], "device", None))
+    status, outs = _lib.shards().shard_call(op, coeff, m, shards,
+                                            None if out is None else list(out), raw)
+    if status != _lib.EC_OK:
+        _lib.check(status, what)
+    return outs
+
+
 def xor_encode(shards: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None,
                stream=None) -> torch.Tensor:
     """Single XOR parity of k equal-size shards."""
-    ptrs, nbytes = _shards(shards, "shards")
-    (out,) = _outputs(None if out is None else [out], 1, nbytes, shards[0].device, "out")
-    _lib.check(_lib.lib().ec_xor_encode(_lib.ptr_array(ptrs), len(ptrs), out.data_ptr(),
-                                        nbytes, stream_handle(stream, shards[0].device)),
-               "ec_xor_encode")
-    return out
+    return _shard_call(0, b"", 1, shards, None if out is None else [out], stream,
+                       "ec_xor_encode")[0]
 
 
 def matvec(coeff: np.ndarray, shards: Sequence[torch.Tensor], out=None, stream=None,
            what: str = "ec_rs_encode") -> List[torch.Tensor]:
     """out[i] = XOR_j coeff[i][j] * shards[j] (bytewise over GF(2^8))."""
     coeff = np.ascontiguousarray(coeff, np.uint8)
+    if coeff.ndim != 2:
+        raise ValueError(f"coefficient matrix must be 2-D, got shape {coeff.shape}")
     m, k = coeff.shape
-    ptrs, nbytes = _shards(shards, "shards")
-    if len(ptrs) != k:
-        raise ValueError(f"coefficient matrix has {k} columns, got {len(ptrs)} shards")
-    outs = _outputs(out, m, nbytes, shards[0].device, "out")
-    fn = _lib.lib().ec_rs_encode if what == "ec_rs_encode" else _lib.lib().ec_rs_decode
-    _lib.check(fn(_lib.u8ptr(coeff), k, m, _lib.ptr_array(ptrs),
-                  _lib.ptr_array([t.data_ptr() for t in outs]), nbytes,
-                  stream_handle(stream, shards[0].device)),
-               what)
-    return outs
+    if len(shards) != k:
+        raise ValueError(f"coefficient matrix has {k} columns, got {len(shards)} shards")
+    if what not in ("ec_rs_encode", "ec_rs_decode"):
+        raise ValueError(f"unknown entry point {what!r}")
+    return _shard_call(1 if what == "ec_rs_encode" else 2, coeff.tobytes(), m, shards, out,
+                       stream, what)
 
 
 class ShardPlan:
@@ -254,9 +280,12 @@ class ShardPlan:
 def rs_encode(shards: Sequence[torch.Tensor], m: int, coeff: Optional[np.ndarray] = None,
               out=None, stream=None) -> List[torch.Tensor]:
     """m Reed-Solomon parity shards of k equal-size data shards."""
+    if coeff is not None:
+        return matvec(coeff, shards, out=out, stream=stream)
     k = len(shards)
-    coeff = cauchy_matrix(k, m) if coeff is None else coeff
-    return matvec(coeff, shards, out=out, stream=stream)
+    if k == 0:
+        raise ValueError("no shards")
+    return _shard_call(1, _cauchy_cached(k, m), m, shards, out, stream, "ec_rs_encode")
 
 
 def reconstruct(codeword: Sequence[Optional[torch.Tensor]], k: int, m: int,

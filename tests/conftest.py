@@ -16,10 +16,11 @@ import __graft_entry__  # noqa: E402
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP) device")
     # Build what is missing (only then): the oracle is a few seconds of gcc,
-    # the HIP library about a minute of hipcc.
+    # the HIP library and its torch binding about two minutes.
     if not os.path.exists(os.path.join(ROOT, "oracle", "libec_oracle.so")):
         subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
-    if not os.path.exists(os.path.join(ROOT, "megatron-lm_amd", "libec_mi355.so")):
+    if not all(os.path.exists(os.path.join(ROOT, "megatron-lm_amd", f))
+               for f in ("libec_mi355.so", "_ec_shards.so")):
         subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "megatron-lm_amd")], check=True)
 
 

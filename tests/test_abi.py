@@ -130,6 +130,38 @@ def test_device_entry_points_reject_bad_arguments(pkg):
     assert L.ec_parity_update(c, 6, 3, one, one, None, one, 1, 64, None) == pkg._lib.EC_EINVAL
 
 
+def test_shard_binding_loads_and_checks_operands(pkg):
+    """The torch-tensor binding of the flat-shard calls loads, maps the same
+    libec_mi355.so as the ctypes binding (one copy in the process), and
+    refuses host tensors, bad coefficient sizes and unknown operations with
+    ValueError before any device work."""
+    import torch
+    B = pkg._lib.shards()
+    pkg._lib.lib()
+    maps = [ln.split() for ln in open("/proc/self/maps") if "libec_mi355.so" in ln]
+    assert {ln[-1] for ln in maps} == {os.path.realpath(pkg._lib.LIB_PATH)}
+    assert sum(1 for ln in maps if int(ln[2], 16) == 0) == 1  # mapped once
+    host = [torch.zeros(64, dtype=torch.uint8) for _ in range(6)]
+    coeff = oracle.cauchy(6, 3).tobytes()
+    for args in ((B.ENCODE, coeff, 3, host), (B.XOR, b"", 1, host),
+                 (B.ENCODE, coeff[:-1], 3, host), (B.DECODE, coeff, 0, host),
+                 (7, coeff, 3, host), (B.ENCODE, coeff, 3, [])):
+        with pytest.raises(ValueError):
+            B.shard_call(*args)
+    with pytest.raises(ValueError, match="device"):
+        pkg.rs_encode(host, 3)
+    with pytest.raises(ValueError, match="columns"):
+        pkg.matvec(oracle.cauchy(6, 3), host[:5])
+
+
+def test_missing_shard_binding_fails_loudly(pkg, monkeypatch):
+    import torch
+    monkeypatch.setattr(pkg._lib, "_shards_mod", None)
+    monkeypatch.setattr(pkg._lib, "SHARDS_PATH", "/nonexistent/_ec_shards.so")
+    with pytest.raises(pkg.ECLibraryMissing):
+        pkg.rs_encode([torch.zeros(64, dtype=torch.uint8)] * 6, 3)
+
+
 def test_missing_library_fails_loudly(pkg, monkeypatch):
     monkeypatch.setattr(pkg._lib, "_lib", None)
     monkeypatch.setattr(pkg._lib, "LIB_PATH", "/nonexistent/libec_mi355.so")

@@ -716,3 +716,59 @@ def test_shard_plan_matches_oracle(pkg, dev, n, offset):
     assert _eq(xp()[0], oracle.xor_encode(d2[:4]))
     for p, w in zip(enc(), oracle.rs_encode(C, d2)):
         assert _eq(p, w)
+
+
+def test_eager_binding_streams_and_operand_checks(pkg, dev):
+    """The eager flat calls (the torch-tensor binding): outputs allocated or
+    given, torch's current stream inside a stream context or an explicit
+    stream, byte-equal to the oracle; operands on the wrong device kind,
+    non-contiguous or of unequal size are refused before any launch."""
+    rng = np.random.default_rng(11)
+    n = (1 << 18) + 3
+    d = _host(rng, 6, n)
+    dd = _to_dev(d, dev)
+    C = oracle.cauchy(6, 3)
+    want = oracle.rs_encode(C, d)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        assert pkg._lib.shards().current_stream(dev.index) == side.cuda_stream
+        par = pkg.rs_encode(dd, 3)
+        out = [torch.full((n,), 7, dtype=torch.uint8, device=dev) for _ in range(3)]
+        pkg.matvec(C, dd, out=out)
+        x = pkg.xor_encode(dd[:5])
+    assert pkg._lib.shards().current_stream(dev.index) == \
+        torch.cuda.current_stream(dev).cuda_stream
+    side.synchronize()
+    for a, b, w in zip(par, out, want):
+        assert np.array_equal(a.cpu().numpy(), w)
+        assert np.array_equal(b.cpu().numpy(), w)
+    assert np.array_equal(x.cpu().numpy(), oracle.xor_encode(d[:5]))
+    for t in out:
+        t.zero_()
+    torch.cuda.synchronize()
+    pkg.rs_encode(dd, 3, out=out, stream=side)
+    side.synchronize()
+    for b, w in zip(out, want):
+        assert np.array_equal(b.cpu().numpy(), w)
+    rec = pkg.reconstruct([None if g in (0, 5, 8) else t for g, t in enumerate(dd + out)], 6, 3)
+    torch.cuda.synchronize()
+    assert np.array_equal(rec[0].cpu().numpy(), d[0])
+    assert np.array_equal(rec[5].cpu().numpy(), d[5])
+    assert np.array_equal(rec[8].cpu().numpy(), want[2])
+    bad = [
+        dd[:5] + [torch.from_numpy(d[5])],                          # a host tensor
+        dd[:5] + [torch.empty(2 * n, dtype=torch.uint8, device=dev)[::2]],  # strided
+        dd[:5] + [torch.empty(n + 1, dtype=torch.uint8, device=dev)],       # one byte more
+    ]
+    for shards in bad:
+        with pytest.raises(ValueError):
+            pkg.rs_encode(shards, 3)
+    with pytest.raises(ValueError):
+        pkg.matvec(C, dd, out=out[:2])
+    with pytest.raises(ValueError):
+        pkg.matvec(C, dd, out=out[:2] + [torch.empty(n - 1, dtype=torch.uint8, device=dev)])
+    with pytest.raises(ValueError):
+        pkg.xor_encode(dd, out=torch.empty(n, dtype=torch.uint8))
+    with pytest.raises(TypeError):
+        pkg.rs_encode(dd[:5] + [d[5]], 3)
