@@ -133,6 +133,8 @@ int ec_rs_decode(const uint8_t* rows, int k, int e,
  *   d_data_len[s*k + j]    valid bytes of that unit (<= unit_bytes); the
  *                          rest of the unit is taken as zeros
  *   d_parity_ptrs[s*m + i] device address of parity unit i (unit_bytes)
+ * The arrays are dense: the kernels read every entry of a stripe, also the
+ * length of an absent unit (ignored).
  * unit_bytes must be a multiple of 16 (EC_EALIGN otherwise) and at most
  * 2 GiB (EC_ERANGE).  Units and
  * parity units at 16-byte-aligned addresses take the vector path; others are
@@ -189,7 +191,9 @@ int ec_decode_batched(const uint8_t* rows, int k, int e,
  *   parity_i ^= XOR_j coeff[i*k+j] * (new_j ^ old_j)
  * for every unit j whose d_new_ptrs[s*k+j] is non-zero (0 = unchanged unit,
  * skipped).  d_old_ptrs holds the previous contents of the same units and
- * d_len their valid bytes; d_parity_ptrs as in ec_encode_batched.  Stripes
+ * d_len their valid bytes (dense arrays, as in ec_encode_batched: the entries
+ * of unchanged units are read and ignored); d_parity_ptrs as in
+ * ec_encode_batched.  Stripes
  * must be distinct (each parity unit is read-modified-written by one
  * workgroup).  Same alignment rules and limits as ec_encode_batched.  Serves repeated
  * manager.save calls (checkpointing.py:538-541) when only part of the state

@@ -11,7 +11,7 @@ namespace {
 // ------------------------------------------------ batched stripe kernels --
 // One workgroup per span of tiles (n_stripes x blocks_per_unit spans),
 // stripe-major: in launch order consecutive workgroups stream adjacent bytes
-// of the same k units; units of kSliceMinUnit and more are dealt in kSlices
+// of the same k units; units of kSliceMinUnit and more are dealt in 8
 // interleaved slices instead (SpanGrid).  The descriptor of a stripe is uniform
 // across the workgroup (scalar loads).
 //
@@ -42,6 +42,7 @@ struct BatchArgs {
   uint32_t tiles_per_unit;   // tiles of B*U*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
+  FastDiv by_blocks;         // division by blocks_per_unit
   SpanGrid grid;             // n_stripes * blocks_per_unit spans
 };
 
@@ -180,39 +181,62 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   // return before any work.
   const uint32_t b = span_of(a.grid);
   if (b >= a.grid.n_spans) return;
-  __shared__ PermTab tab[M][K];
-  stage_tables<K, M>(tab, a.tab);
   // Workgroup b covers tiles [t0, t1) of one stripe: the descriptor loads and
-  // table staging are paid once per span, not once per 4-8 KiB tile.
-  const uint32_t s = b / a.blocks_per_unit;
+  // table staging are paid once per span, not once per tile.
+  const uint32_t s = fast_div(b, a.by_blocks);
   const uint32_t t0 = (b - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
-  // Stripe-uniform facts (scalar registers): addresses, valid lengths, and
-  // whether everything is 16-byte aligned.
+  // The stripe's descriptors (uniform: scalar registers).  The arrays are
+  // dense ([n_stripes][K] / [n_stripes][M]), so every entry of the stripe is
+  // read unconditionally and the reads merge into a few wide scalar loads in
+  // flight together.  Reading a length only after its address had come back
+  // non-zero made every unit a dependent round trip: RS(8,2) over 4 MiB units
+  // then spent most of a one-tile workgroup's life in its preamble.
+  uint64_t dp[K], pp[M], cp[K];
+  uint32_t dl[K], pl[M];
+#pragma unroll
+  for (int j = 0; j < K; ++j) dp[j] = a.dptr[(uint64_t)s * K + j];
+#pragma unroll
+  for (int j = 0; j < K; ++j) dl[j] = a.dlen[(uint64_t)s * K + j];
+#pragma unroll
+  for (int i = 0; i < M; ++i) pp[i] = a.pptr[(uint64_t)s * M + i];
+  if (a.olen) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) pl[i] = a.olen[(uint64_t)s * M + i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < M; ++i) pl[i] = a.unit_bytes;
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) cp[j] = COPY ? a.cptr[(uint64_t)s * K + j] : 0u;
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  // Addresses, valid lengths (0 for an absent unit or output), and whether
+  // everything is 16-byte aligned.
   const uint8_t* d[K];
   uint32_t len[K];
   bool in_aligned = true, out_aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    d[j] = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * K + j]);
-    const uint32_t l = d[j] ? a.dlen[(uint64_t)s * K + j] : 0u;
+    d[j] = reinterpret_cast<const uint8_t*>(dp[j]);
+    const uint32_t l = dp[j] ? dl[j] : 0u;
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    in_aligned &= (reinterpret_cast<uintptr_t>(d[j]) & 15u) == 0;
+    in_aligned &= (dp[j] & 15u) == 0;
   }
   uint8_t* p[M];
   uint32_t olen[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
-    const uint32_t l = p[i] ? (a.olen ? a.olen[(uint64_t)s * M + i] : a.unit_bytes) : 0u;
+    p[i] = reinterpret_cast<uint8_t*>(pp[i]);
+    const uint32_t l = pp[i] ? pl[i] : 0u;
     olen[i] = l < a.unit_bytes ? l : a.unit_bytes;
-    out_aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
+    out_aligned &= (pp[i] & 15u) == 0;
   }
   uint8_t* c[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    c[j] = COPY ? reinterpret_cast<uint8_t*>(a.cptr[(uint64_t)s * K + j]) : nullptr;
-    out_aligned &= (reinterpret_cast<uintptr_t>(c[j]) & 15u) == 0;
+    c[j] = reinterpret_cast<uint8_t*>(cp[j]);
+    out_aligned &= (cp[j] & 15u) == 0;
   }
   constexpr uint32_t kTileBytes = B * U * 16u;
   for (uint32_t t = t0; t < t1; ++t) {
@@ -268,8 +292,9 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  a.by_blocks = make_fastdiv(a.blocks_per_unit);
   const uint64_t blocks = span_grid(a.grid, (uint64_t)n_stripes * a.blocks_per_unit,
-                                    slices_for(unit_bytes));
+                                    slice_shift_for(unit_bytes));
   if (blocks == 0) return EC_ERANGE;
   hipLaunchKernelGGL((batched_kernel<K, M, U, COPY, B>), dim3((unsigned)blocks), dim3(B), 0,
                      st, a);

@@ -37,6 +37,7 @@
 #include <stdint.h>
 
 #include "ec_mi355.h"
+#include "fastdiv.h"
 #include "gf256.h"
 
 namespace ec {
@@ -356,7 +357,7 @@ inline unsigned grid_of(uint64_t n16, int lanes) {
 // ----------------------------------------- grid order of batched launches --
 // A batched launch codes n_spans spans (a span: consecutive tiles of one
 // stripe, one workgroup each), stripe-major.  Units of kSliceMinUnit and
-// more are walked in kSlices interleaved slices: the dispatcher deals
+// more are walked in 8 (2^kSliceShift) interleaved slices: the dispatcher deals
 // consecutive workgroups to the 8 XCDs in turn, so workgroup b taking span
 // (b % 8) * slice_spans + b / 8 makes each XCD stream its own eighth of the
 // stripes, and the work in flight sits at 8 unrelated offsets of the units
@@ -368,32 +369,36 @@ inline unsigned grid_of(uint64_t n16, int lanes) {
 // -> 0.700, 32 MiB 0.621 -> 0.720, 64 MiB 0.685 -> 0.724; below 2 MiB the
 // slices cost 2-5 % (1 MiB 0.776 -> 0.734), and 64 KiB units gained nothing.
 constexpr uint32_t kSliceMinUnit = 2u << 20;
-constexpr uint32_t kSlices = 8;
+constexpr uint32_t kSliceShift = 3;  // kSlices = 8
 
 struct SpanGrid {
   uint32_t n_spans;      // the spans to code
-  uint32_t slices;       // interleaved slices (1: launch order)
+  uint32_t slice_shift;  // log2 of the interleaved slices (0: launch order)
   uint32_t slice_spans;  // ceil(n_spans / slices)
 };
 
-inline uint32_t slices_for(uint32_t unit_bytes) {
-  return unit_bytes >= kSliceMinUnit ? kSlices : 1u;
+inline uint32_t slice_shift_for(uint32_t unit_bytes) {
+  return unit_bytes >= kSliceMinUnit ? kSliceShift : 0u;
 }
 
-// Fills g for `spans` (>= 1) spans in `slices` (>= 1) slices and returns the
-// grid, rounded up to whole slices; 0 when it exceeds 2^31 - 1 workgroups.
-inline uint64_t span_grid(SpanGrid& g, uint64_t spans, uint32_t slices) {
+// Fills g for `spans` (>= 1) spans in 2^shift slices and returns the grid,
+// rounded up to whole slices; 0 when it exceeds 2^31 - 1 workgroups.
+inline uint64_t span_grid(SpanGrid& g, uint64_t spans, uint32_t shift) {
+  const uint64_t slices = 1ull << shift;
   if (spans + slices - 1 > 0x7fffffffull) return 0;
   g.n_spans = (uint32_t)spans;
-  g.slices = slices;
-  g.slice_spans = (uint32_t)((spans + slices - 1) / slices);
-  return (uint64_t)g.slice_spans * slices;
+  g.slice_shift = shift;
+  g.slice_spans = (uint32_t)((spans + slices - 1) >> shift);
+  return (uint64_t)g.slice_spans << shift;
 }
 
 // The span of this workgroup; n_spans or more for the few workgroups past
 // the last span, which return before any work (uniform per workgroup).
+// With shift 0 it is blockIdx.x; no branch, so the launch scalars load
+// together.
 __device__ __forceinline__ uint32_t span_of(const SpanGrid& g) {
-  return g.slices == 1 ? blockIdx.x : (blockIdx.x % g.slices) * g.slice_spans + blockIdx.x / g.slices;
+  const uint32_t b = blockIdx.x;
+  return (b & ((1u << g.slice_shift) - 1u)) * g.slice_spans + (b >> g.slice_shift);
 }
 
 inline bool fast_shape(int k, int m) { return k <= kFastMaxK && m <= kFastMaxM; }

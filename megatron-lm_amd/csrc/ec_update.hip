@@ -24,6 +24,7 @@ struct UpdateArgs {
   uint32_t tiles_per_unit;   // tiles of B*16 bytes in a unit (B lanes)
   uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
   uint32_t blocks_per_unit;
+  FastDiv by_blocks;  // division by blocks_per_unit
 };
 
 // Incremental update: each workgroup walks a span of tiles of one changed
@@ -33,11 +34,22 @@ struct UpdateArgs {
 // aligned, takes plain vector loads, any other tile the byte-granular path.
 template <int K, int M, int B>
 __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
-  __shared__ PermTab tab[M][K];
-  stage_tables<K, M>(tab, a.tab);
-  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t s = fast_div(blockIdx.x, a.by_blocks);
   const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
+  // The stripe's descriptors, every entry read unconditionally (the arrays
+  // are dense) so that the reads merge into wide scalar loads in flight
+  // together rather than one dependent round trip per unit.
+  uint64_t np[K], op[K];
+  uint32_t nl[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) np[j] = a.nptr[(uint64_t)s * K + j];
+#pragma unroll
+  for (int j = 0; j < K; ++j) op[j] = a.optr[(uint64_t)s * K + j];
+#pragma unroll
+  for (int j = 0; j < K; ++j) nl[j] = a.len[(uint64_t)s * K + j];
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
   const uint8_t* nw[K];
   const uint8_t* od[K];
   uint32_t len[K];
@@ -45,9 +57,9 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
   bool aligned = true, in_aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    nw[j] = reinterpret_cast<const uint8_t*>(a.nptr[(uint64_t)s * K + j]);
-    od[j] = nw[j] ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * K + j]) : nullptr;
-    const uint32_t l = nw[j] ? a.len[(uint64_t)s * K + j] : 0u;
+    nw[j] = reinterpret_cast<const uint8_t*>(np[j]);
+    od[j] = np[j] ? reinterpret_cast<const uint8_t*>(op[j]) : nullptr;
+    const uint32_t l = np[j] ? nl[j] : 0u;
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
     if (nw[j]) {
       full = len[j] < full ? len[j] : full;
@@ -135,6 +147,7 @@ struct BatchWideArgs {
   uint32_t tiles_per_unit;
   uint32_t tiles_per_block;
   uint32_t blocks_per_unit;
+  FastDiv by_blocks;  // division by blocks_per_unit
   int k;
 };
 
@@ -160,10 +173,14 @@ __device__ __forceinline__ bool stage_wide(WideStripe<M>& w, const BatchWideArgs
   const uint32_t t = threadIdx.x;
   for (uint32_t i = t; i < (uint32_t)(M * k); i += B) w.tab[i] = dev_perm_tab(a.coeff[i]);
   if (t < (uint32_t)k) {
+    // Dense arrays: the length (and in an update the old unit's address) is
+    // read together with the address, not after it.
     const uint8_t* d = reinterpret_cast<const uint8_t*>(a.dptr[(uint64_t)s * k + t]);
-    const uint32_t l = d ? a.dlen[(uint64_t)s * k + t] : 0u;
-    const uint8_t* o = update && d ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * k + t])
-                                   : nullptr;
+    const uint32_t dl = a.dlen[(uint64_t)s * k + t];
+    const uint8_t* o0 = update ? reinterpret_cast<const uint8_t*>(a.optr[(uint64_t)s * k + t])
+                               : nullptr;
+    const uint32_t l = d ? dl : 0u;
+    const uint8_t* o = d ? o0 : nullptr;
     w.d[t] = d;
     w.o[t] = o;
     w.len[t] = l < a.unit_bytes ? l : a.unit_bytes;
@@ -202,7 +219,7 @@ template <int M, int B>
 __global__ void __launch_bounds__(B) batched_wide_kernel(const BatchWideArgs a) {
   constexpr uint32_t kWideTile = B * 16u;
   __shared__ WideStripe<M> w;
-  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t s = fast_div(blockIdx.x, a.by_blocks);
   const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
   const bool misaligned = stage_wide<M, B>(w, a, s, false);
@@ -253,7 +270,7 @@ template <int M, int B>
 __global__ void __launch_bounds__(B) update_wide_kernel(const BatchWideArgs a) {
   constexpr uint32_t kWideTile = B * 16u;
   __shared__ WideStripe<M> w;
-  const uint32_t s = blockIdx.x / a.blocks_per_unit;
+  const uint32_t s = fast_div(blockIdx.x, a.by_blocks);
   const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
   stage_wide<M, B>(w, a, s, true);
@@ -306,6 +323,7 @@ int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* op
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  a.by_blocks = make_fastdiv(a.blocks_per_unit);
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
   hipLaunchKernelGGL((update_kernel<K, M, B>), dim3((unsigned)blocks), dim3(B), 0, st, a);
@@ -344,6 +362,7 @@ int launch_batched_wide_b(const uint8_t* coeff, int k, const uint64_t* dptr, con
   if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
+  a.by_blocks = make_fastdiv(a.blocks_per_unit);
   const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
   if (blocks > 0x7fffffffull) return EC_ERANGE;
   if (update)
