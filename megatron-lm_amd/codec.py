@@ -199,6 +199,12 @@ def _shard_call(op: int, coeff: bytes, m: int, shards, out, stream, what: str):
                                             None if out is None else list(out), raw)
     if status != _lib.EC_OK:
         _lib.check(status, what)
+    if stream is not None and out is None:
+        # Outputs allocated here belong to torch's current stream; the kernel
+        # writes them on `stream`, so their memory must not be handed out
+        # again before that stream's work is done.
+        for t in outs:
+            t.record_stream(stream)
     return outs
 
 

@@ -748,9 +748,11 @@ def test_eager_binding_streams_and_operand_checks(pkg, dev):
         t.zero_()
     torch.cuda.synchronize()
     pkg.rs_encode(dd, 3, out=out, stream=side)
+    par2 = pkg.rs_encode(dd, 3, stream=side)  # allocated on torch's stream, written on side
     side.synchronize()
-    for b, w in zip(out, want):
+    for b, c, w in zip(out, par2, want):
         assert np.array_equal(b.cpu().numpy(), w)
+        assert np.array_equal(c.cpu().numpy(), w)
     rec = pkg.reconstruct([None if g in (0, 5, 8) else t for g, t in enumerate(dd + out)], 6, 3)
     torch.cuda.synchronize()
     assert np.array_equal(rec[0].cpu().numpy(), d[0])
