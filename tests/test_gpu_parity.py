@@ -774,3 +774,25 @@ def test_eager_binding_streams_and_operand_checks(pkg, dev):
         pkg.xor_encode(dd, out=torch.empty(n, dtype=torch.uint8))
     with pytest.raises(TypeError):
         pkg.rs_encode(dd[:5] + [d[5]], 3)
+
+
+def test_flat_kernels_past_the_grid_cap(pkg, dev):
+    """Shards of 16 GiB + 4 KiB + 48 B: more 16-byte chunks than the flat
+    kernels' one-pass grid covers (2^24 one-wavefront workgroups), so the
+    grid-stride loop runs a second time for the last chunks, and a byte tail
+    follows.  XOR(2) and RS(2,1) with unit coefficients both equal a ^ b."""
+    n = (16 << 30) + 4096 + 48
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    a = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 256, generator=g)
+    b = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 256, generator=g)
+    want = torch.bitwise_xor(a, b)
+    x = pkg.xor_encode([a, b])
+    torch.cuda.synchronize()
+    assert torch.equal(x, want)
+    del x
+    r = pkg.matvec(np.ones((1, 2), np.uint8), [a, b])[0]
+    torch.cuda.synchronize()
+    assert torch.equal(r, want)
+    del a, b, r, want
+    torch.cuda.empty_cache()
