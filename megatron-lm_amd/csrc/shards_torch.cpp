@@ -1,5 +1,6 @@
 // Python binding of the flat-shard entry points (ec_xor_encode, ec_rs_encode,
-// ec_rs_decode) that takes torch tensors directly.
+// ec_rs_decode) that takes torch tensors directly, and the address and size
+// reads of the ragged tensor lists.
 //
 // codec.matvec / codec.xor_encode call it once per call: the checks on every
 // shard (device tensor, contiguous, one device, one byte size), the host
@@ -110,6 +111,32 @@ py::tuple shard_call(int64_t op, const std::string& coeff, int64_t m,
   return py::make_tuple(status, outs);
 }
 
+// (base addresses, byte sizes) of a list of tensors that must all be
+// contiguous device tensors on device `device`, as two byte strings of
+// uint64 / int64 (numpy reads them without a copy).  The ragged-list
+// layout checks every tensor of a checkpoint (thousands) on the path that
+// holds training: here that costs the list conversion, about 0.1 us per
+// tensor, against 0.36 us in Python.
+py::tuple spans(const std::vector<at::Tensor>& tensors, int64_t device) {
+  const size_t n = tensors.size();
+  std::string base(n * sizeof(uint64_t), '\0'), size(n * sizeof(int64_t), '\0');
+  auto* b = reinterpret_cast<uint64_t*>(&base[0]);
+  auto* z = reinterpret_cast<int64_t*>(&size[0]);
+  for (size_t i = 0; i < n; ++i) {
+    const at::Tensor& t = tensors[i];
+    if (!t.is_cuda())
+      throw py::value_error("tensors[" + std::to_string(i) + "] must be a device (HIP) tensor");
+    if (!t.is_contiguous())
+      throw py::value_error("tensors[" + std::to_string(i) + "] must be contiguous");
+    if (t.device().index() != device)
+      throw py::value_error("tensors[" + std::to_string(i) + "] is on " + t.device().str() +
+                            ", the other operands on cuda:" + std::to_string(device));
+    b[i] = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(t.data_ptr()));
+    z[i] = static_cast<int64_t>(t.nbytes());
+  }
+  return py::make_tuple(py::bytes(base), py::bytes(size));
+}
+
 // The raw handle of torch's current stream on a device (-1: the current
 // device), as codec.stream_handle passes it to the C ABI.
 int64_t current_stream(int64_t device) {
@@ -127,4 +154,5 @@ PYBIND11_MODULE(_ec_shards, mod) {
   mod.def("shard_call", &shard_call, py::arg("op"), py::arg("coeff"), py::arg("m"),
           py::arg("shards"), py::arg("out") = py::none(), py::arg("stream") = py::none());
   mod.def("current_stream", &current_stream, py::arg("device") = -1);
+  mod.def("spans", &spans, py::arg("tensors"), py::arg("device"));
 }

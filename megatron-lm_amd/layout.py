@@ -86,26 +86,17 @@ def _upload(a: np.ndarray, device) -> torch.Tensor:
 def _spans(tensors: Sequence[torch.Tensor], device) -> Tuple[np.ndarray, np.ndarray]:
     """(base addresses, byte sizes) of contiguous HIP tensors on ``device``.
     A save codes thousands of tensors on the path that holds training, so the
-    checks and the reads go through ``map`` over the unbound Tensor methods
-    (about 0.36 us per tensor against 0.5 us for a loop); a tensor that fails
-    a check gets codec._dev's error."""
-    idx = torch.device(device).index if device is not None else None
-    T = torch.Tensor
+    checks and the reads run in the torch-tensor binding (about 0.1 us per
+    tensor); a tensor that fails a check raises ValueError (TypeError for
+    something that is not a tensor)."""
     tensors = list(tensors)
-    try:
-        ok = idx is not None and all(map(T.is_contiguous, tensors)) and \
-            list(map(T.get_device, tensors)).count(idx) == len(tensors)
-    except TypeError:   # not a tensor
-        ok = False
-    if not ok:
-        for i, t in enumerate(tensors):
-            if not isinstance(t, T) or t.get_device() != idx or idx is None or \
-                    not t.is_contiguous():
-                _dev(t, f"tensors[{i}]", device)
-                raise ValueError(f"tensors[{i}] is not a contiguous tensor on {device}")
-    ptrs = np.array(list(map(T.data_ptr, tensors)), np.uint64).reshape(-1)
-    sizes = np.array(list(map(T.nbytes.__get__, tensors)), np.int64).reshape(-1)
-    return ptrs, sizes
+    idx = torch.device(device).index if device is not None else None
+    if idx is None:
+        if tensors:
+            _dev(tensors[0], "tensors[0]", device)
+        raise ValueError(f"tensors must be on a HIP device, not {device}")
+    base, size = _lib.shards().spans(tensors, idx)
+    return np.frombuffer(base, np.uint64), np.frombuffer(size, np.int64)
 
 
 @dataclass
