@@ -796,3 +796,85 @@ def test_flat_kernels_past_the_grid_cap(pkg, dev):
     assert torch.equal(r, want)
     del a, b, r, want
     torch.cuda.empty_cache()
+
+
+def _random_case(seed):
+    """Shape of one randomized batched case: a code (mostly the unrolled
+    k <= 16, m <= 4 kernels, sometimes a wide one), a unit size that is any
+    multiple of 16 up to 20 KiB (so tiles end anywhere inside a unit),
+    ragged tensor sizes from 1 byte to a few units, views at odd offsets or
+    separate allocations."""
+    r = np.random.default_rng(seed)
+    if r.random() < 0.8:
+        k, m = int(r.integers(1, 17)), int(r.integers(1, 5))
+    else:
+        k, m = int(r.integers(2, 21)), int(r.integers(5, 9))
+    unit = 16 * int(r.integers(1, 1281))
+    return r, k, m, unit, int(r.integers(1, 25)), bool(r.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_batched_random_layouts(pkg, dev, seed):
+    """Seeded random layouts through every batched entry point: the encode
+    and the copying encode against the oracle (parity, zero-padded copies),
+    a decode of a random set of at most m lost positions restores the data
+    and the parity, and an update of random units equals a fresh encode."""
+    from megatron_lm_amd import _lib
+    r, k, m, unit, n_tensors, misalign = _random_case(seed)
+    host, tensors = _ragged_device(r, dev, n_tensors, int(r.integers(2, 4 * unit + 2)), misalign)
+    pset = pkg.encode(tensors, k, m, unit)
+    lay = pset.layout
+    S = lay.n_stripes
+    torch.cuda.synchronize()
+    want_par = _oracle_layout_parity(lay, host, unit)
+    assert np.array_equal(pset.parity.cpu().numpy(), want_par), (k, m, unit)
+    # copying encode into a stripe-major block
+    block = torch.full((S, k + m, unit), 0xC3, dtype=torch.uint8, device=dev)
+    base = np.uint64(block.data_ptr())
+    rows = np.arange(S, dtype=np.uint64)[:, None] * np.uint64((k + m) * unit)
+    cp = base + rows + np.arange(k, dtype=np.uint64)[None, :] * np.uint64(unit)
+    pp = base + rows + (np.arange(m, dtype=np.uint64)[None, :] + np.uint64(k)) * np.uint64(unit)
+    d_cp = torch.from_numpy(np.ascontiguousarray(cp).view(np.int64)).to(dev)
+    d_pp = torch.from_numpy(np.ascontiguousarray(pp).view(np.int64)).to(dev)
+    _lib.check(_lib.lib().ec_encode_batched_copy(
+        _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
+        d_pp.data_ptr(), d_cp.data_ptr(), S, unit, None), "ec_encode_batched_copy")
+    torch.cuda.synchronize()
+    got = block.cpu().numpy()
+    assert np.array_equal(got[:, k:], want_par)
+    for s in range(S):
+        for j in range(k):
+            u = s * k + j
+            want = np.zeros(unit, np.uint8)
+            if u < lay.n_units:
+                t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+                piece = host[t][i * unit: (i + 1) * unit]
+                want[: piece.size] = piece
+            assert np.array_equal(got[s, j], want), (s, j)
+    del block, d_cp, d_pp
+    # decode of a random lost set
+    lost = sorted(int(x) for x in r.choice(k + m, int(r.integers(1, m + 1)), replace=False))
+    par_ref = pset.parity.clone()
+    for s in range(S):
+        for pos in lost:
+            u = s * k + pos
+            if pos < k and u < lay.n_units:
+                lay.unit_view(u).fill_(0xA5)
+            elif pos >= k:
+                pset.parity[s, pos - k].fill_(0x5A)
+    pkg.decode(pset, lost)
+    torch.cuda.synchronize()
+    for h, t in zip(host, tensors):
+        assert np.array_equal(t.cpu().numpy(), h), lost
+    assert torch.equal(pset.parity, par_ref), lost
+    # update of random units
+    changed = np.sort(r.choice(lay.n_units, max(1, lay.n_units // 4), replace=False))
+    olds = []
+    for u in changed:
+        v = lay.unit_view(int(u))
+        olds.append(v.clone())
+        v.copy_(torch.from_numpy(r.integers(0, 256, v.numel(), dtype=np.uint8)))
+    pkg.update(pset, changed, olds)
+    fresh = lay.encode()
+    torch.cuda.synchronize()
+    assert torch.equal(pset.parity, fresh)
