@@ -878,3 +878,46 @@ def test_batched_random_layouts(pkg, dev, seed):
     fresh = lay.encode()
     torch.cuda.synchronize()
     assert torch.equal(pset.parity, fresh)
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_flat_random_shards(pkg, dev, seed):
+    """Seeded random flat-shard calls: codes from RS(1,1) to RS(24,8) and
+    XOR, sizes from 1 byte to ~300 KiB (vector body and byte tail), each
+    shard and output at its own offset 0..15 (aligned, one shared
+    misalignment, or mixed: the realigning and the byte kernels), with random
+    coefficient matrices as well as the Cauchy block; the encode against the
+    oracle and a reconstruction of a random erasure set."""
+    r = np.random.default_rng(1000 + seed)
+    k = int(r.integers(1, 25))
+    m = int(r.integers(1, 9)) if r.random() < 0.3 else int(r.integers(1, 5))
+    n = int(r.integers(1, 300_000))
+    mode = int(r.integers(0, 3))   # 0 aligned, 1 one shared offset, 2 mixed offsets
+    shared = int(r.integers(1, 16))
+
+    def off():
+        return 0 if mode == 0 else shared if mode == 1 else int(r.integers(0, 16))
+    d = _host(r, k, n)
+    dd = [_to_dev([a], dev, off())[0] for a in d]
+    if r.random() < 0.25:
+        C = r.integers(0, 256, (m, k), dtype=np.uint8)
+        out = [_to_dev([np.zeros(n, np.uint8)], dev, off())[0] for _ in range(m)]
+        got = pkg.matvec(C, dd, out=out)
+        want = oracle.rs_encode(C, d)
+        for g, w in zip(got, want):
+            assert _eq(g, w), (k, m, n, mode)
+        return
+    C = oracle.cauchy(k, m)
+    out = [_to_dev([np.zeros(n, np.uint8)], dev, off())[0] for _ in range(m)]
+    par = pkg.rs_encode(dd, m, out=out)
+    want = oracle.rs_encode(C, d)
+    for g, w in zip(par, want):
+        assert _eq(g, w), (k, m, n, mode)
+    if m == 1:
+        assert _eq(pkg.xor_encode(dd), oracle.xor_encode(d)), (k, n, mode)
+    lost = sorted(int(x) for x in r.choice(k + m, int(r.integers(1, m + 1)), replace=False))
+    cw = dd + par
+    rec = pkg.reconstruct([None if g in lost else t for g, t in enumerate(cw)], k, m)
+    full = d + want
+    for g in lost:
+        assert _eq(rec[g], full[g]), (k, m, n, mode, lost)
