@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 LIB_NAME = "libec_mi355.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
@@ -125,6 +126,7 @@ def lib() -> ctypes.CDLL:
 SHARDS_NAME = "_ec_shards"
 SHARDS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), SHARDS_NAME + ".so")
 _shards_mod = None
+_shards_lock = threading.Lock()
 
 
 def shards():
@@ -134,18 +136,22 @@ def shards():
     global _shards_mod
     if _shards_mod is not None:
         return _shards_mod
-    lib()  # the C library first: checks its ABI version and gives the extension its symbols
-    if not os.path.exists(SHARDS_PATH):
-        raise ECLibraryMissing(
-            f"{SHARDS_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
-    import importlib.machinery
-    import importlib.util
-    import torch  # noqa: F401  (the extension needs torch's libraries loaded)
-    loader = importlib.machinery.ExtensionFileLoader(SHARDS_NAME, SHARDS_PATH)
-    spec = importlib.util.spec_from_file_location(SHARDS_NAME, SHARDS_PATH, loader=loader)
-    mod = importlib.util.module_from_spec(spec)
-    loader.exec_module(mod)
-    _shards_mod = mod
+    with _shards_lock:   # one load, also when threads race to the first call
+        if _shards_mod is not None:
+            return _shards_mod
+        lib()  # the C library first: checks its ABI version and gives the extension its symbols
+        if not os.path.exists(SHARDS_PATH):
+            raise ECLibraryMissing(
+                f"{SHARDS_PATH} is not built; run `python -c 'import __graft_entry__ as g; "
+                "g.build()'`")
+        import importlib.machinery
+        import importlib.util
+        import torch  # noqa: F401  (the extension needs torch's libraries loaded)
+        loader = importlib.machinery.ExtensionFileLoader(SHARDS_NAME, SHARDS_PATH)
+        spec = importlib.util.spec_from_file_location(SHARDS_NAME, SHARDS_PATH, loader=loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+        _shards_mod = mod
     return mod
 
 
