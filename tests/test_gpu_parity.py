@@ -921,3 +921,45 @@ def test_flat_random_shards(pkg, dev, seed):
     full = d + want
     for g in lost:
         assert _eq(rec[g], full[g]), (k, m, n, mode, lost)
+
+
+def test_host_threads_on_their_own_streams(pkg, dev):
+    """The library is re-entrant: four host threads, each on a stream of its
+    own, run 10 rounds of a flat RS(6,3) encode and a batched RS(8,2) encode
+    of their own tensors at the same time; every result equals the oracle's."""
+    import threading
+    rng = np.random.default_rng(8)
+    n, unit = (1 << 20) + 3, 8192
+    jobs = []
+    for _ in range(4):
+        d = _host(rng, 6, n)
+        host, tensors = _ragged_device(rng, dev, 12, 5 * unit, misalign=True)
+        jobs.append((d, _to_dev(d, dev), host, tensors))
+    torch.cuda.synchronize()
+    results, errors = [None] * 4, []
+
+    def work(i):
+        try:
+            s = torch.cuda.Stream(dev)
+            with torch.cuda.stream(s):
+                for _ in range(10):
+                    par = pkg.rs_encode(jobs[i][1], 3)
+                    lay = pkg.StripeLayout(jobs[i][3], 8, 2, unit)
+                    bpar = lay.encode()
+            s.synchronize()
+            results[i] = ([p.cpu().numpy() for p in par], lay, bpar.cpu().numpy())
+        except Exception as e:  # reported below, in the test's thread
+            errors.append((i, e))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    C = oracle.cauchy(6, 3)
+    for (d, _, host, _), (par, lay, bpar) in zip(jobs, results):
+        for p, w in zip(par, oracle.rs_encode(C, d)):
+            assert np.array_equal(p, w)
+        assert np.array_equal(bpar, _oracle_layout_parity(lay, host, unit))
