@@ -44,6 +44,8 @@ struct BatchArgs {
   uint32_t blocks_per_unit;  // ceil(tiles_per_unit / tiles_per_block)
   FastDiv by_blocks;         // division by blocks_per_unit
   SpanGrid grid;             // n_stripes * blocks_per_unit spans
+  uint32_t rest_groups;      // workgroups per stripe of batched_rest_kernel
+  FastDiv by_groups;         // division by rest_groups
 };
 
 // Zeros in device memory, read-only: on the fast path a unit that ended
@@ -174,6 +176,112 @@ __device__ __forceinline__ void tile_edge(const BatchArgs<K, M>& a, uint32_t s, 
   }
 }
 
+// A stripe's descriptors (uniform: scalar registers).  The arrays are dense
+// ([n_stripes][K] / [n_stripes][M]), so every entry of the stripe is read
+// unconditionally and the reads merge into a few wide scalar loads in flight
+// together.  Reading a length only after its address had come back non-zero
+// made every unit a dependent round trip: RS(8,2) over 4 MiB units then spent
+// most of a one-tile workgroup's life in its preamble.
+template <int K, int M, bool COPY>
+struct StripeDesc {
+  uint64_t dp[K], pp[M], cp[K];
+  uint32_t dl[K], pl[M];
+};
+
+template <int K, int M, bool COPY>
+__device__ __forceinline__ void read_stripe(StripeDesc<K, M, COPY>& r, const BatchArgs<K, M>& a,
+                                            uint32_t s) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) r.dp[j] = a.dptr[(uint64_t)s * K + j];
+#pragma unroll
+  for (int j = 0; j < K; ++j) r.dl[j] = a.dlen[(uint64_t)s * K + j];
+#pragma unroll
+  for (int i = 0; i < M; ++i) r.pp[i] = a.pptr[(uint64_t)s * M + i];
+  if (a.olen) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) r.pl[i] = a.olen[(uint64_t)s * M + i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < M; ++i) r.pl[i] = a.unit_bytes;
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) r.cp[j] = COPY ? a.cptr[(uint64_t)s * K + j] : 0u;
+}
+
+// Addresses, valid lengths (0 for an absent unit or output), and whether
+// everything is 16-byte aligned.
+template <int K, int M, bool COPY>
+struct Stripe {
+  const uint8_t* d[K];
+  uint32_t len[K];
+  uint8_t* p[M];
+  uint32_t olen[M];
+  uint8_t* c[K];
+  bool in_aligned, out_aligned;
+};
+
+template <int K, int M, bool COPY>
+__device__ __forceinline__ void stripe_facts(Stripe<K, M, COPY>& st,
+                                             const StripeDesc<K, M, COPY>& r,
+                                             uint32_t unit_bytes) {
+  st.in_aligned = true;
+  st.out_aligned = true;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    st.d[j] = reinterpret_cast<const uint8_t*>(r.dp[j]);
+    const uint32_t l = r.dp[j] ? r.dl[j] : 0u;
+    st.len[j] = l < unit_bytes ? l : unit_bytes;
+    st.in_aligned &= (r.dp[j] & 15u) == 0;
+  }
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    st.p[i] = reinterpret_cast<uint8_t*>(r.pp[i]);
+    const uint32_t l = r.pp[i] ? r.pl[i] : 0u;
+    st.olen[i] = l < unit_bytes ? l : unit_bytes;
+    st.out_aligned &= (r.pp[i] & 15u) == 0;
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    st.c[j] = reinterpret_cast<uint8_t*>(r.cp[j]);
+    st.out_aligned &= (r.cp[j] & 15u) == 0;
+  }
+}
+
+// Tile t of stripe s through the path its contents need.  A tile is an edge
+// tile when some unit ends strictly inside it or some output does not cover
+// it (or an output is misaligned); a full tile with every unit aligned takes
+// tile_full, one with misaligned units tile_full_realign.
+template <int K, int M, int U, bool COPY, int B>
+__device__ __forceinline__ void code_tile(const BatchArgs<K, M>& a, uint32_t s, uint32_t t,
+                                          const Stripe<K, M, COPY>& st,
+                                          const PermTab (&tab)[M][K]) {
+  constexpr uint32_t kTileBytes = B * U * 16u;
+  const uint32_t base = t * (B * U) + threadIdx.x;
+  const uint32_t lo = t * kTileBytes, hi = lo + kTileBytes;
+  const uint8_t* src[K];
+  uint8_t* dst[M];
+  uint8_t* cpy[K];
+  bool edge = !st.out_aligned;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    src[j] = st.len[j] >= hi ? st.d[j] + lo : g_zero_tile;
+    edge |= st.len[j] > lo && st.len[j] < hi;
+    cpy[j] = st.c[j] ? st.c[j] + lo : nullptr;
+    if (COPY) edge |= st.c[j] && a.unit_bytes < hi;  // a copy always spans the unit
+  }
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    dst[i] = st.p[i] + lo;
+    edge |= st.olen[i] < hi;
+  }
+  if (edge)
+    tile_edge<K, M, U, COPY, B>(a, s, base, tab);
+  else if (st.in_aligned)
+    tile_full<K, M, U, COPY, B>(src, dst, cpy, tab);
+  else
+    tile_full_realign<K, M, U, COPY, B>(src, dst, cpy, tab);
+}
+
 template <int K, int M, int U, bool COPY, int B>
 __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   // The span this workgroup takes (uniform: a scalar branch); the grid is
@@ -186,86 +294,151 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   const uint32_t s = fast_div(b, a.by_blocks);
   const uint32_t t0 = (b - s * a.blocks_per_unit) * a.tiles_per_block;
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
-  // The stripe's descriptors (uniform: scalar registers).  The arrays are
-  // dense ([n_stripes][K] / [n_stripes][M]), so every entry of the stripe is
-  // read unconditionally and the reads merge into a few wide scalar loads in
-  // flight together.  Reading a length only after its address had come back
-  // non-zero made every unit a dependent round trip: RS(8,2) over 4 MiB units
-  // then spent most of a one-tile workgroup's life in its preamble.
-  uint64_t dp[K], pp[M], cp[K];
-  uint32_t dl[K], pl[M];
-#pragma unroll
-  for (int j = 0; j < K; ++j) dp[j] = a.dptr[(uint64_t)s * K + j];
-#pragma unroll
-  for (int j = 0; j < K; ++j) dl[j] = a.dlen[(uint64_t)s * K + j];
-#pragma unroll
-  for (int i = 0; i < M; ++i) pp[i] = a.pptr[(uint64_t)s * M + i];
-  if (a.olen) {
-#pragma unroll
-    for (int i = 0; i < M; ++i) pl[i] = a.olen[(uint64_t)s * M + i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < M; ++i) pl[i] = a.unit_bytes;
-  }
-#pragma unroll
-  for (int j = 0; j < K; ++j) cp[j] = COPY ? a.cptr[(uint64_t)s * K + j] : 0u;
+  StripeDesc<K, M, COPY> r;
+  read_stripe(r, a, s);
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
-  // Addresses, valid lengths (0 for an absent unit or output), and whether
-  // everything is 16-byte aligned.
-  const uint8_t* d[K];
-  uint32_t len[K];
-  bool in_aligned = true, out_aligned = true;
+  Stripe<K, M, COPY> st;
+  stripe_facts(st, r, a.unit_bytes);
+  for (uint32_t t = t0; t < t1; ++t) code_tile<K, M, U, COPY, B>(a, s, t, st, tab);
+}
+
+// ---- large units: the full tiles and the rest, as two kernels ----------
+// For RS(8,2) over units of kSplitMinUnit up to kSplitMaxUnit (not for the
+// copying encode) a launch is two kernels over disjoint tiles of every
+// stripe:
+//  - batched_full_kernel, one workgroup per tile in launch order, codes the
+//    tiles of an aligned stripe before its first unit end and after its last
+//    one (tile_split), as far as every output covers them, and returns at
+//    once on the others: nothing but the vector path, and the compiler
+//    spreads its unit loads between the GF arithmetic;
+//  - batched_rest_kernel, rest_groups workgroups per stripe, codes the other
+//    tiles through code_tile.  A stripe of whole units (a rank's buffer cut
+//    into units: every stripe but the last) returns after reading its
+//    descriptors.
+// Measured on MI355X over 20.8 GB of data, fraction of the 8 TB/s roofline
+// at 2 / 4 / 8 MiB units, the single kernel (8 slices) -> the two kernels,
+// each pair from one box:
+//   RS(8,2)   0.785 0.763 0.762 -> 0.831 0.818 0.787
+//   RS(6,2)   0.791 0.773 0.774 -> 0.817 0.788 0.753
+//   RS(4,2)   0.831 0.800 0.797 -> 0.833 0.805 0.782
+//   RS(4,1)   0.809 0.796 0.779 -> 0.806 0.790 0.779
+//   RS(6,3)   0.817 0.795 0.785 -> 0.781 0.763 0.725
+//   RS(10,2)  0.776 0.750 0.752 -> 0.723 0.720 0.695
+//   RS(16,1)  0.748 0.736 0.739 -> 0.709 0.666 0.628
+//   RS(5,4)   0.742 0.723 0.716 -> 0.612 0.611 0.591
+// so only RS(8,2), the code of a rank's checkpoint buffer and the one code
+// that gains at every size, takes the split (split_pays).  Below 2 MiB its single kernel runs in launch order at
+// 0.82-0.85 and the split gains nothing; at 16 and 32 MiB the split lost
+// (0.662 against 0.714, 0.668 against 0.772).
+constexpr uint32_t kSplitMinUnit = 2u << 20;
+constexpr uint32_t kSplitMaxUnit = 16u << 20;
+
+template <int K, int M>
+constexpr bool split_pays() {
+  return K == 8 && M == 2;
+}
+
+// The tiles of an aligned stripe that hold an end strictly inside them lie
+// in [first_end, last_end] (empty: first_end > last_end); from out_end on some
+// output does not cover the tile (output i covers tile t iff olen[i] >=
+// (t + 1) * kTileBytes).  batched_full_kernel codes the tiles before
+// first_end and those between last_end and out_end, where every unit covers
+// the tile or ended before it (read as zeros) and every output covers it;
+// batched_rest_kernel the others, and every tile of a stripe with a
+// misaligned address.
+struct TileSplit {
+  uint32_t first_end, last_end, out_end;
+};
+
+template <int K, int M, bool COPY, uint32_t kTileBytes>
+__device__ __forceinline__ TileSplit tile_split(const Stripe<K, M, COPY>& st, uint32_t tiles) {
+  TileSplit sp{tiles, 0u, tiles};
+  bool any = false;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    d[j] = reinterpret_cast<const uint8_t*>(dp[j]);
-    const uint32_t l = dp[j] ? dl[j] : 0u;
-    len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    in_aligned &= (dp[j] & 15u) == 0;
+    const bool inside = st.len[j] % kTileBytes != 0;
+    const uint32_t t = st.len[j] / kTileBytes;
+    sp.first_end = inside && t < sp.first_end ? t : sp.first_end;
+    sp.last_end = inside && t > sp.last_end ? t : sp.last_end;
+    any |= inside;
   }
-  uint8_t* p[M];
-  uint32_t olen[M];
+  if (!any) sp.last_end = 0, sp.first_end = tiles;   // no end inside any tile
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    p[i] = reinterpret_cast<uint8_t*>(pp[i]);
-    const uint32_t l = pp[i] ? pl[i] : 0u;
-    olen[i] = l < a.unit_bytes ? l : a.unit_bytes;
-    out_aligned &= (pp[i] & 15u) == 0;
+    const uint32_t t = st.olen[i] / kTileBytes;
+    sp.out_end = t < sp.out_end ? t : sp.out_end;
   }
-  uint8_t* c[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    c[j] = reinterpret_cast<uint8_t*>(cp[j]);
-    out_aligned &= (cp[j] & 15u) == 0;
-  }
-  constexpr uint32_t kTileBytes = B * U * 16u;
-  for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t base = t * (B * U) + threadIdx.x;
-    const uint32_t lo = t * kTileBytes, hi = lo + kTileBytes;
-    // A tile is an edge tile when some unit ends strictly inside it or some
-    // output does not cover it.
+  if (!(st.in_aligned && st.out_aligned)) sp.out_end = 0;   // nothing for the vector kernel
+  return sp;
+}
+
+// Whether batched_full_kernel codes tile t.
+__device__ __forceinline__ bool vector_tile(const TileSplit& sp, uint32_t t) {
+  return t < sp.out_end && (t < sp.first_end || t > sp.last_end);
+}
+
+template <int K, int M, int B>
+__global__ void __launch_bounds__(B) batched_full_kernel(const BatchArgs<K, M> a) {
+  // One tile per workgroup (the launcher splits only when tiles_per_block
+  // is 1).
+  const uint32_t b = span_of(a.grid);
+  if (b >= a.grid.n_spans) return;
+  const uint32_t s = fast_div(b, a.by_blocks);
+  const uint32_t t = b - s * a.blocks_per_unit;
+  StripeDesc<K, M, false> r;
+  read_stripe(r, a, s);
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  Stripe<K, M, false> st;
+  stripe_facts(st, r, a.unit_bytes);
+  constexpr uint32_t kTileBytes = B * 16u;
+  const TileSplit sp = tile_split<K, M, false, kTileBytes>(st, a.tiles_per_unit);
+  // A loop of zero or one tile rather than a return and straight-line code:
+  // in this form the compiler interleaves the unit loads with the GF
+  // arithmetic (RS(8,2): 122 VGPRs against 142 with the loads hoisted), and
+  // RS(8,2) over 4 MiB units runs at 0.82 of the roofline against 0.79.
+  const uint32_t t_end = vector_tile(sp, t) ? t + 1 : t;
+  if (t >= t_end) return;   // the rest kernel's
+  for (uint32_t u = t; u < t_end; ++u) {
+    const uint32_t lo = u * kTileBytes, hi = lo + kTileBytes;
     const uint8_t* src[K];
     uint8_t* dst[M];
     uint8_t* cpy[K];
-    bool edge = !out_aligned;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      src[j] = len[j] >= hi ? d[j] + lo : g_zero_tile;
-      edge |= len[j] > lo && len[j] < hi;
-      cpy[j] = c[j] ? c[j] + lo : nullptr;
-      if (COPY) edge |= c[j] && a.unit_bytes < hi;  // a copy always spans the unit
+      src[j] = st.len[j] >= hi ? st.d[j] + lo : g_zero_tile;
+      cpy[j] = nullptr;
     }
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-      dst[i] = p[i] + lo;
-      edge |= olen[i] < hi;
-    }
-    if (edge)
-      tile_edge<K, M, U, COPY, B>(a, s, base, tab);
-    else if (in_aligned)
-      tile_full<K, M, U, COPY, B>(src, dst, cpy, tab);
-    else
-      tile_full_realign<K, M, U, COPY, B>(src, dst, cpy, tab);
+    for (int i = 0; i < M; ++i) dst[i] = st.p[i] + lo;
+    tile_full<K, M, 1, false, B>(src, dst, cpy, tab);
+  }
+}
+
+template <int K, int M, int B>
+__global__ void __launch_bounds__(B) batched_rest_kernel(const BatchArgs<K, M> a) {
+  const uint32_t s = fast_div(blockIdx.x, a.by_groups);
+  const uint32_t g = blockIdx.x - s * a.rest_groups;
+  StripeDesc<K, M, false> r;
+  read_stripe(r, a, s);
+  Stripe<K, M, false> st;
+  stripe_facts(st, r, a.unit_bytes);
+  constexpr uint32_t kTileBytes = B * 16u;
+  const uint32_t tiles = a.tiles_per_unit;
+  const TileSplit sp = tile_split<K, M, false, kTileBytes>(st, tiles);
+  // The tiles batched_full_kernel leaves: [first_end, last_end] below
+  // out_end, then [out_end, tiles), numbered in that order and dealt round
+  // robin to the stripe's workgroups.
+  const uint32_t mid_end = sp.last_end < sp.out_end ? sp.last_end + 1 : sp.out_end;
+  const uint32_t mid = sp.first_end < mid_end ? mid_end - sp.first_end : 0u;
+  const uint32_t total = mid + (tiles - sp.out_end);
+  if (g >= total) return;
+  __shared__ PermTab tab[M][K];
+  stage_tables<K, M>(tab, a.tab);
+  for (uint32_t n = g; n < total; n += a.rest_groups) {
+    const uint32_t t = n < mid ? sp.first_end + n : sp.out_end + (n - mid);
+    code_tile<K, M, 1, false, B>(a, s, t, st, tab);
   }
 }
 
@@ -293,9 +466,28 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
   a.tiles_per_block = (uint32_t)tpb;
   a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
   a.by_blocks = make_fastdiv(a.blocks_per_unit);
+  const bool split = !COPY && U == 1 && split_pays<K, M>() && a.tiles_per_block == 1 &&
+                     unit_bytes >= kSplitMinUnit && unit_bytes < kSplitMaxUnit;
   const uint64_t blocks = span_grid(a.grid, (uint64_t)n_stripes * a.blocks_per_unit,
-                                    slice_shift_for(unit_bytes));
+                                    split ? 0u : slice_shift_for(unit_bytes));
   if (blocks == 0) return EC_ERANGE;
+  if constexpr (!COPY && U == 1 && split_pays<K, M>()) {
+    if (split) {
+      // Enough rest workgroups to fill the chip when whole stripes are
+      // misaligned (about 8192 in all), at most one per tile.
+      uint64_t groups = (8192u + (uint64_t)n_stripes - 1) / n_stripes;
+      if (groups > a.tiles_per_unit) groups = a.tiles_per_unit;
+      a.rest_groups = (uint32_t)groups;
+      a.by_groups = make_fastdiv(a.rest_groups);
+      const uint64_t rest_blocks = (uint64_t)n_stripes * groups;
+      if (rest_blocks > 0x7fffffffull) return EC_ERANGE;
+      hipLaunchKernelGGL((batched_full_kernel<K, M, B>), dim3((unsigned)blocks), dim3(B), 0,
+                         st, a);
+      hipLaunchKernelGGL((batched_rest_kernel<K, M, B>), dim3((unsigned)rest_blocks),
+                         dim3(B), 0, st, a);
+      return hip_status();
+    }
+  }
   hipLaunchKernelGGL((batched_kernel<K, M, U, COPY, B>), dim3((unsigned)blocks), dim3(B), 0,
                      st, a);
   return hip_status();

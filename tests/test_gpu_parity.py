@@ -377,6 +377,73 @@ def test_batched_sliced_order(pkg, dev, k, m, unit, misalign, lost):
     assert np.array_equal(par.cpu().numpy(), want_par)
 
 
+def _padded_flat_parity(pkg, lay, s):
+    """Parity of stripe s by the flat kernel over zero-padded copies of its
+    units (absent units are zeros)."""
+    unit = lay.unit_bytes
+    shards = []
+    for j in range(lay.k):
+        pad = torch.zeros(unit, dtype=torch.uint8, device=lay.device)
+        u = s * lay.k + j
+        if u < lay.n_units:
+            v = lay.unit_view(u)
+            pad[: v.numel()].copy_(v)
+        shards.append(pad)
+    return torch.stack(pkg.rs_encode(shards, lay.m, coeff=lay.coeff))
+
+
+@pytest.mark.parametrize("unit,offsets", [
+    (2 << 20, (0,)),                       # aligned: the full-tile kernel and the rest
+    ((4 << 20) + 1024, (0, 16)),           # 4097 tiles a unit, views 16 bytes in
+    (8 << 20, (0, 16, 5)),                 # aligned and misaligned stripes in one launch
+    ((16 << 20) - 16, (0,))])              # the largest split unit, a short last tile
+def test_batched_full_and_rest_kernels(pkg, dev, unit, offsets):
+    """RS(8,2) over units of 2 to 16 MiB runs as two kernels: one codes the
+    tiles where every unit and output is whole or already ended, the other
+    the tiles that hold a unit's end, the outputs' short tails and every tile
+    of a stripe with a misaligned address.  Tensors end on tile boundaries,
+    inside tiles, on unit boundaries and one byte in; the last stripe has
+    absent units.  The parity equals the flat kernel's over zero-padded units
+    (and the oracle's at 2 MiB), and two lost positions (two data units; a
+    data unit and a parity) decode back through the same split."""
+    k, m = 8, 2
+    sizes = [3 * unit, 2 * unit + 1024 * 37, unit + 777, 5 * unit - 16, 4096, 1,
+             2 * unit + 3000, unit - 1024 * 5]
+    g = torch.Generator(device=dev)
+    g.manual_seed(unit)
+    tensors = []
+    for i, n in enumerate(sizes):
+        off = offsets[i % len(offsets)]
+        buf = torch.empty(n + off, dtype=torch.uint8, device=dev)
+        v = buf[off:]
+        v.copy_(torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g))
+        tensors.append(v)
+    keep = [t.clone() for t in tensors]
+    lay = pkg.StripeLayout(tensors, k, m, unit)
+    assert lay.n_units % k != 0   # the last stripe has absent units
+    par = lay.encode()
+    for s in range(lay.n_stripes):
+        assert torch.equal(par[s], _padded_flat_parity(pkg, lay, s)), s
+    if unit == 2 << 20:
+        torch.cuda.synchronize()
+        host = [t.cpu().numpy() for t in tensors]
+        assert np.array_equal(par.cpu().numpy(), _oracle_layout_parity(lay, host, unit))
+    par_ref = par.clone()
+    for lost in ((2, 7), (1, 9)):
+        for s in range(lay.n_stripes):
+            for pos in lost:
+                u = s * k + pos
+                if pos < k and u < lay.n_units:
+                    lay.unit_view(u).fill_(0xA5)
+                elif pos >= k:
+                    par[s, pos - k].fill_(0x5A)
+        lay.decode(par, list(lost))
+        torch.cuda.synchronize()
+        for t, want in zip(tensors, keep):
+            assert torch.equal(t, want), lost
+        assert torch.equal(par, par_ref), lost
+
+
 @pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 2048, False), (6, 3, 20480, False),
                                                 (12, 4, 4096, True), (8, 2, 16384, True)])
 def test_batched_update_equals_reencode(pkg, dev, k, m, unit, misalign):
