@@ -615,20 +615,22 @@ def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
     calibration kernel of known traffic); config 5 (RS(12,4), 3,000 ragged
     tensors, 64 KiB units): encode, copying encode into one stripe-major
     (stripes, 16, 64 KiB) block (the snapshot's kernel), decode of lost positions 1, 7, 12,
-    14, 1 % update; config 4 (RS(8,2), 20.8 GB buffer, 4 MiB units) encode.
-    Prints the launch groups with their algorithmic bytes as JSON."""
+    14, 1 % update; config 4 (RS(8,2), 20.8 GB buffer, 4 MiB units) encode,
+    which the library runs as two kernels per launch (the full tiles and the
+    rest).  Prints the launch groups with their algorithmic bytes and kernel
+    dispatches as JSON."""
     import numpy as np
     import torch
     from megatron_lm_amd.checkpoint import GpuSliceCodec
     groups = []
 
-    def three(name, fn, read, write):
+    def three(name, fn, read, write, kernels=1):
         torch.cuda.synchronize()
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
-        groups.append({"name": name, "launches": 3, "read_bytes": int(read),
-                       "write_bytes": int(write)})
+        groups.append({"name": name, "launches": 3, "dispatches": 3 * kernels,
+                       "read_bytes": int(read), "write_bytes": int(write)})
 
     shard = 256 * MiB
     src = torch.empty(shard, dtype=torch.uint8, device=dev).random_(0, 256)
@@ -677,7 +679,7 @@ def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
     del host
     lay = pkg.StripeLayout([buf], 8, 2, 4 * MiB)
     par = lay.alloc_parity()
-    three("c4_encode", lambda: lay.encode(par), lay.data_bytes, par.numel())
+    three("c4_encode", lambda: lay.encode(par), lay.data_bytes, par.numel(), kernels=2)
     print(json.dumps({"mode": "batched-pmc", "groups": groups}), flush=True)
     return 0
 
