@@ -1,6 +1,7 @@
-// ec_batched.h — the fixed-size batched stripe kernel (batched_kernel) and
-// its launcher, shared by the plain encode/decode (ec_batched.hip) and the
-// copying encode (ec_batched_copy.hip).
+// ec_batched.h — the fixed-size batched stripe kernel (batched_kernel), the
+// two-kernel form for large RS(8,2) units (batched_full_kernel and
+// batched_rest_kernel) and their launcher, shared by the plain encode/decode
+// (ec_batched.hip) and the copying encode (ec_batched_copy.hip).
 #pragma once
 
 #include "ec_device.h"
@@ -12,7 +13,8 @@ namespace {
 // One workgroup per span of tiles (n_stripes x blocks_per_unit spans),
 // stripe-major: in launch order consecutive workgroups stream adjacent bytes
 // of the same k units; units of kSliceMinUnit and more are dealt in 8
-// interleaved slices instead (SpanGrid).  The descriptor of a stripe is uniform
+// interleaved slices instead (SpanGrid), except where the launcher splits the
+// launch in two (RS(8,2), see split_pays).  The descriptor of a stripe is uniform
 // across the workgroup (scalar loads).
 //
 // The product launches one-wavefront workgroups with one 16-byte chunk per
