@@ -561,6 +561,75 @@ def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
             "encode_frac_of_mix_bound": round(enc_traffic_gbs / bound, 4)}
 
 
+def stripe_layouts(pkg, synth, dev, seed: int) -> dict:
+    """RS(6,3) over config 2's bytes (6 x 256 MiB) placed three ways, each
+    timed like the headline (clock settle, then HIP events around 50
+    back-to-back launches) and checked byte for byte against the flat
+    kernel's parity:
+      flat          the flat kernel on six separate 256 MiB shards, parity in
+                    three separate 256 MiB buffers;
+      cut           the batched kernel over the same six shards cut into
+                    units (stripe s = the s-th unit of every shard, parity
+                    written into the three separate buffers the same way):
+                    the flat kernel's access order;
+      contiguous    the batched kernel over one 1.5 GiB buffer holding the
+                    same units stripe after stripe (the six units of a stripe
+                    adjacent, then its three parity units adjacent), the
+                    layout the checkpoint path builds from a rank's tensors.
+    Fraction of the 8 TB/s roofline from the 9 x 256 MiB of HBM traffic."""
+    import numpy as np
+    import torch
+    k, m, shard = 6, 3, 256 * MiB
+    host = synth.rs_shards(seed, shard, k)
+    data = [torch.from_numpy(h).to(dev) for h in host]
+    del host
+    coeff = pkg.cauchy_matrix(k, m)
+    par = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
+    L = pkg._lib.lib()
+    st = pkg.codec.stream_handle(None, dev)
+    traffic = (k + m) * shard
+
+    def rate(fn):
+        settle(fn, 0.3)
+        _, ev = timed(fn, 50, 5)
+        return {"us": round(ev * 1e3, 1),
+                "frac": round(traffic / (ev * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
+
+    out = {"flat": rate(lambda: pkg.rs_encode(data, m, out=par))}
+    torch.cuda.synchronize()
+    for U in (64 << 10, 1 * MiB):
+        n = shard // U
+        views = [data[j][s * U:(s + 1) * U] for s in range(n) for j in range(k)]
+        cut = pkg.StripeLayout(views, k, m, U, coeff)
+        cut_par = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
+        pp = (np.array([p.data_ptr() for p in cut_par], dtype=np.uint64)[None, :]
+              + np.arange(n, dtype=np.uint64)[:, None] * np.uint64(U))
+        d_pp = torch.from_numpy(np.ascontiguousarray(pp).view(np.int64)).to(dev)
+
+        def cut_encode():
+            pkg._lib.check(L.ec_encode_batched(
+                pkg._lib.u8ptr(cut.coeff), k, m, cut.d_ptrs.data_ptr(), cut.d_len.data_ptr(),
+                d_pp.data_ptr(), n, U, st), "ec_encode_batched")
+        tag = f"{U >> 10}KiB"
+        out[f"cut_{tag}"] = rate(cut_encode)
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(cut_par, par)):
+            raise AssertionError(f"cut layout ({tag} units): parity differs from the flat kernel")
+        del cut, cut_par, d_pp, views
+        buf = torch.stack([d.view(n, U) for d in data], dim=1).reshape(-1)
+        cont = pkg.StripeLayout([buf], k, m, U, coeff)
+        cont_par = cont.alloc_parity()
+        out[f"contiguous_{tag}"] = rate(lambda: cont.encode(cont_par))
+        torch.cuda.synchronize()
+        for i in range(m):
+            if not torch.equal(cont_par[:, i].reshape(-1), par[i]):
+                raise AssertionError(f"contiguous layout ({tag} units): parity {i} differs")
+        del buf, cont, cont_par
+        torch.cuda.empty_cache()
+    log(f"stripe layouts: {out}")
+    return out
+
+
 def small_shards(pkg, dev) -> dict:
     """RS(6,3) over small shards, where the per-call host work competes with
     the kernel: back-to-back eager calls (matvec into given outputs, and
@@ -868,7 +937,7 @@ def main() -> int:
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
     ap.add_argument("--mode", choices=["full", "headline", "decode", "flat-kernels", "pmc",
                                        "batched", "batched-kernels", "batched-pmc",
-                                       "gf-variants", "train", "small-shards"],
+                                       "gf-variants", "train", "small-shards", "layout"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); flat-kernels: configs 2, 3 "
@@ -881,7 +950,9 @@ def main() -> int:
                          "counter runs; gf-variants: "
                          "the v_perm GF multiply against LDS log/exp tables; train: a training "
                          "loop with synchronous and with snapshot checkpoint saves; "
-                         "small-shards: RS(6,3) over 1 and 4 MiB shards, eager and planned")
+                         "small-shards: RS(6,3) over 1 and 4 MiB shards, eager and planned; "
+                         "layout: RS(6,3) over config 2's bytes as six shards, cut into "
+                         "units, and stripe-contiguous")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the erasure-coding path has no multi-GPU "
@@ -911,6 +982,10 @@ def main() -> int:
         return gf_variants(pkg, synth, dev, args.seed, min(args.steps, 50))
     if args.mode == "small-shards":
         print(json.dumps({"mode": args.mode, **small_shards(pkg, dev)}), flush=True)
+        return 0
+    if args.mode == "layout":
+        print(json.dumps({"mode": args.mode, **stripe_layouts(pkg, synth, dev, args.seed)}),
+              flush=True)
         return 0
     if args.mode == "train":
         print(json.dumps({"mode": "train", **training_with_checkpoints(pkg, dev)}), flush=True)
