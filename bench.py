@@ -4,7 +4,8 @@ Headline metric: RS(6,3) encode GB/s of data bytes over six 256 MiB shards of
 serialized fp32 optimizer state, inputs resident in HBM, and its HBM roofline
 fraction.  Also measured in the same run and reported under
 "also": RS(6,3) decode with 3 seeded erasures, XOR parity of 4 x 64 MiB bf16
-shards, the batched configurations, the encode's interference with a GEMM
+shards, the headline's bytes coded in two other layouts (cut into units, and
+stripe-contiguous), the batched configurations, the encode's interference with a GEMM
 load, the checkpoint staging path and snapshot saves, a training loop with
 periodic saves, and a streaming copy as the practical bandwidth ceiling.  The
 CPU baseline is the repo's multithreaded SIMD CPU encoder (the reference ships
@@ -561,8 +562,8 @@ def skeleton_ceilings(pkg, dev, shard: int, enc_traffic_gbs: float) -> dict:
             "encode_frac_of_mix_bound": round(enc_traffic_gbs / bound, 4)}
 
 
-def stripe_layouts(pkg, synth, dev, seed: int) -> dict:
-    """RS(6,3) over config 2's bytes (6 x 256 MiB) placed three ways, each
+def stripe_layouts(pkg, dev, data) -> dict:
+    """RS(6,3) over config 2's bytes (``data``: 6 x 256 MiB) placed three ways, each
     timed like the headline (clock settle, then HIP events around 50
     back-to-back launches) and checked byte for byte against the flat
     kernel's parity:
@@ -580,9 +581,7 @@ def stripe_layouts(pkg, synth, dev, seed: int) -> dict:
     import numpy as np
     import torch
     k, m, shard = 6, 3, 256 * MiB
-    host = synth.rs_shards(seed, shard, k)
-    data = [torch.from_numpy(h).to(dev) for h in host]
-    del host
+    assert len(data) == k and all(d.numel() == shard for d in data)
     coeff = pkg.cauchy_matrix(k, m)
     par = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
     L = pkg._lib.lib()
@@ -626,6 +625,8 @@ def stripe_layouts(pkg, synth, dev, seed: int) -> dict:
                 raise AssertionError(f"contiguous layout ({tag} units): parity {i} differs")
         del buf, cont, cont_par
         torch.cuda.empty_cache()
+    del par
+    torch.cuda.empty_cache()
     log(f"stripe layouts: {out}")
     return out
 
@@ -984,8 +985,8 @@ def main() -> int:
         print(json.dumps({"mode": args.mode, **small_shards(pkg, dev)}), flush=True)
         return 0
     if args.mode == "layout":
-        print(json.dumps({"mode": args.mode, **stripe_layouts(pkg, synth, dev, args.seed)}),
-              flush=True)
+        data = [torch.from_numpy(h).to(dev) for h in synth.rs_shards(args.seed, 256 * MiB, 6)]
+        print(json.dumps({"mode": args.mode, **stripe_layouts(pkg, dev, data)}), flush=True)
         return 0
     if args.mode == "train":
         print(json.dumps({"mode": "train", **training_with_checkpoints(pkg, dev)}), flush=True)
@@ -1066,6 +1067,7 @@ def main() -> int:
                           "copy_GBps": round(2 * src.numel() / (cev * 1e-3) / 1e9, 1)}), flush=True)
         return 0
     small = small_shards(pkg, dev)
+    layouts = stripe_layouts(pkg, dev, data)
 
     gemm = GemmLoad(dev)
     batched = {} if args.no_batched else batched_configs(
@@ -1135,6 +1137,7 @@ def main() -> int:
             "decode_kernel_us": round(dev_ms * 1e3, 2),
             "xor_4x64MiB_GBps": round(xor_gbs, 2), "xor_kernel_us": round(xev * 1e3, 2),
             **small,
+            "stripe_layouts": layouts,
             **batched,
             **over,
             "copy_ceiling_GBps": round(copy_gbs, 1),
