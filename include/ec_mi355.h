@@ -127,8 +127,10 @@ int ec_rs_decode(const uint8_t* rows, int k, int e,
                  const uint8_t* const* d_survivors, uint8_t* const* d_out,
                  uint64_t nbytes, ec_stream_t stream);
 
-/* Batched ragged encode: one launch over n_stripes stripes of k units of
- * unit_bytes each.  Device arrays, row-major:
+/* Batched ragged encode: one call over n_stripes stripes of k units of
+ * unit_bytes each (one kernel launch on `stream`; two for k = 8, m = 2 over
+ * units of 2 MiB up to 16 MiB, which code disjoint tiles).  Device arrays,
+ * row-major:
  *   d_data_ptrs[s*k + j]   device address of unit j of stripe s (0 = absent)
  *   d_data_len[s*k + j]    valid bytes of that unit (<= unit_bytes); the
  *                          rest of the unit is taken as zeros

@@ -56,11 +56,14 @@ def test_graph_replays_match_eager(pkg, dev):
             assert np.array_equal(rec[r].cpu().numpy(), ref), f"replay {rep} shard {gidx}"
 
 
-def test_graph_batched_encode_and_decode(pkg, dev):
+@pytest.mark.parametrize("unit", [16384, 2 << 20])
+def test_graph_batched_encode_and_decode(pkg, dev, unit):
     """The batched launcher over a ragged list in a graph: encode, then
     decode of two lost positions, replayed after eager changes to the data;
-    each replay checked against an eager encode and the tensors' bytes."""
-    k, m, unit = 8, 2, 16384
+    each replay checked against an eager encode and the tensors' bytes.
+    RS(8,2) over 2 MiB units runs as two kernels per call (full tiles, then
+    the rest), both captured."""
+    k, m = 8, 2
     rng = np.random.default_rng(21)
     sizes = rng.integers(1, 5 * unit, 40)
     tensors = [torch.from_numpy(rng.integers(0, 256, int(n), dtype=np.uint8)).to(dev)
