@@ -444,6 +444,54 @@ def test_batched_full_and_rest_kernels(pkg, dev, unit, offsets):
         assert torch.equal(par, par_ref), lost
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_batched_full_and_rest_random(pkg, dev, seed):
+    """Seeded random RS(8,2) layouts on the two-kernel launch: a unit size
+    anywhere from 2 MiB to 16 MiB - 16 B in 16-byte steps (tiles end anywhere
+    inside a unit), 2 to 9 tensors of 1 byte to 3 units at offsets of 0, 16,
+    48 bytes or an odd one from 256-byte boundaries of one arena, with 4 KiB
+    of 0xC3 between them.  The parity equals the flat kernel's over
+    zero-padded units (a kernel reading past a unit's end would fold the
+    0xC3 bytes in), and two random lost positions decode back with every
+    byte of the arena, the gaps included, as before."""
+    k, m = 8, 2
+    r = np.random.default_rng(1000 + seed)
+    unit = 16 * int(r.integers((2 << 20) // 16, (16 << 20) // 16))
+    n_tensors = int(r.integers(2, 10))
+    sizes = [int(r.integers(1, 3 * unit)) for _ in range(n_tensors)]
+    offs = [int(r.choice([0, 0, 16, 48, int(r.integers(1, 16))])) for _ in range(n_tensors)]
+    starts, pos = [], 0
+    for n, off in zip(sizes, offs):
+        starts.append(pos + off)
+        pos = (pos + off + n + 4096 + 255) // 256 * 256
+    arena = torch.full((pos,), 0xC3, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    tensors = []
+    for n, a in zip(sizes, starts):
+        v = arena[a:a + n]
+        v.copy_(torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g))
+        tensors.append(v)
+    arena_before = arena.clone()
+    lay = pkg.StripeLayout(tensors, k, m, unit)
+    par = lay.encode()
+    for s in range(lay.n_stripes):
+        assert torch.equal(par[s], _padded_flat_parity(pkg, lay, s)), (seed, unit, s)
+    par_ref = par.clone()
+    lost = sorted(int(x) for x in r.choice(k + m, 2, replace=False))
+    for s in range(lay.n_stripes):
+        for pos in lost:
+            u = s * k + pos
+            if pos < k and u < lay.n_units:
+                lay.unit_view(u).fill_(0xA5)
+            elif pos >= k:
+                par[s, pos - k].fill_(0x5A)
+    lay.decode(par, lost)
+    torch.cuda.synchronize()
+    assert torch.equal(arena, arena_before), (seed, unit, lost)
+    assert torch.equal(par, par_ref), (seed, unit, lost)
+
+
 @pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 2048, False), (6, 3, 20480, False),
                                                 (12, 4, 4096, True), (8, 2, 16384, True)])
 def test_batched_update_equals_reencode(pkg, dev, k, m, unit, misalign):
