@@ -217,12 +217,13 @@ def test_golden_rs(pkg, dev, name):
 
 def _ragged_device(rng, dev, n_tensors, max_bytes, misalign=False):
     """Device tensors of random byte sizes (some zero-length-free, some odd),
-    optionally as views at odd offsets of one arena."""
+    optionally as views at odd offsets of one arena whose gaps hold 0xC3 (a
+    kernel reading past a tensor's end would fold them into the parity)."""
     sizes = rng.integers(1, max_bytes, n_tensors)
     host = [rng.integers(0, 256, s, dtype=np.uint8) for s in sizes]
     if not misalign:
         return host, [torch.from_numpy(h).to(dev) for h in host]
-    arena = torch.empty(int(sizes.sum()) + 7 * n_tensors, dtype=torch.uint8, device=dev)
+    arena = torch.full((int(sizes.sum()) + 7 * n_tensors,), 0xC3, dtype=torch.uint8, device=dev)
     views, off = [], 0
     for h in host:
         off += int(rng.integers(0, 7))
