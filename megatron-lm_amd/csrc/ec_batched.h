@@ -322,6 +322,7 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
 // at 2 / 4 / 8 MiB units, the single kernel (8 slices) -> the two kernels,
 // each pair from one box:
 //   RS(8,2)   0.785 0.763 0.762 -> 0.831 0.818 0.787
+//   RS(8,1)   0.759 0.745 0.742 -> 0.760 0.733 0.686
 //   RS(6,2)   0.791 0.773 0.774 -> 0.817 0.788 0.753
 //   RS(4,2)   0.831 0.800 0.797 -> 0.833 0.805 0.782
 //   RS(4,1)   0.809 0.796 0.779 -> 0.806 0.790 0.779
