@@ -87,7 +87,12 @@ __device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uin
 // XOR parity: one-wavefront workgroups in launch order, one chunk per lane.
 // Measured on MI355X for XOR(4) (HBM traffic, GB/s): over 64 MiB shards 6482
 // vs 6357 for the former 512-lane workgroups with two chunks per lane (6399
-// with 128 lanes, 6288 with 256); over 256 MiB 6621 vs 6555.
+// with 128 lanes, 6288 with 256); over 256 MiB 6621 vs 6555.  The parity
+// store is a plain one for k > 1: XOR(4) 6470 against 6360 with a streaming
+// store over 64 MiB shards, 6806 against 6443 over 256 MiB.  rs_kernel is the
+// other way round (RS(6,3) over 256 MiB shards: streaming parity stores 0.80
+// of the roofline, plain 0.76), and so is the copy (k = 1, 3 % faster
+// streaming).
 constexpr int kXorBlock = 64;
 
 template <int K>
