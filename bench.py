@@ -72,6 +72,16 @@ def settle(fn, seconds: float):
             return (time.perf_counter() - t0) * 1e3, n
 
 
+def steady(fn, steps: int, warmup: int, seconds: float = 0.3):
+    """timed() after ``seconds`` of back-to-back calls (settle): the batched
+    configurations start right after seconds of host-side data generation,
+    and without it their first timed launches run on a GPU still raising its
+    clocks (config 5's encode ran 4.59 ms at the start of a 10-launch window
+    and 4.14 at its end)."""
+    settle(fn, seconds)
+    return timed(fn, steps, warmup)
+
+
 def launch_spread(fn, steps: int):
     """Per-launch durations (ms) of `steps` back-to-back calls of fn(), from
     an event pair around each call on torch's current stream: the median
@@ -226,7 +236,7 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
         f"{time.perf_counter() - t1:.1f} s")
     lay = pkg.StripeLayout([buf], 8, 2, 4 * MiB)
     par = lay.alloc_parity()
-    w, e = timed(lambda: lay.encode(par), 10, 2)
+    w, e = steady(lambda: lay.encode(par), 10, 2)
     if cpu_seconds:
         _, hptr, hlen = stripe_descriptors([host.ctypes.data], [host.size], 8, 4 * MiB)
         sample = list(range(16)) + [lay.n_stripes - 1]
@@ -254,7 +264,7 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     tensors, views = ragged_tensors(synth, dev, seed, with_host=True)
     lay = pkg.StripeLayout(tensors, 12, 4, 64 << 10)
     par = lay.alloc_parity()
-    w, e = timed(lambda: lay.encode(par), 10, 2)
+    w, e = steady(lambda: lay.encode(par), 10, 2)
     if cpu_seconds:
         _, hptr, hlen = stripe_descriptors([v.ctypes.data for v in views],
                                            [v.size for v in views], 12, 64 << 10)
@@ -285,7 +295,7 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
         raise AssertionError("incremental update differs from a full re-encode")
     del fresh
     # each further run folds the same delta in again (timing only)
-    w, e = timed(lambda: lay.run(plan), 10, 2)
+    w, e = steady(lambda: lay.run(plan), 10, 2)
     changed_bytes = int(lay.host_len.reshape(-1)[changed].sum())
     upd_traffic = 2 * changed_bytes + 2 * plan.n_stripes * 4 * (64 << 10)
     out["update_1pct_changed_GB"] = round(changed_bytes / 1e9, 3)
@@ -294,7 +304,7 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     lay.encode(par)  # repeated update runs toggled the parity; restore it
     lost = [1, 7, 12, 14]
     dplan = lay.plan_decode(par, lost)
-    w, e = timed(lambda: lay.run(dplan), 5, 1)
+    w, e = steady(lambda: lay.run(dplan), 5, 1)
     k5, S5, U5 = 12, lay.n_stripes, 64 << 10
     surv = [p for p in range(16) if p not in lost][:k5]
     hl = lay.host_len.astype(np.int64)
@@ -315,7 +325,7 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
         pkg._lib.check(L.ec_encode_batched_copy(
             pkg._lib.u8ptr(lay.coeff), 12, 4, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
             bp.data_ptr(), gp.data_ptr(), S5, U5, st), "ec_encode_batched_copy")
-    w, e = timed(copy_encode, 5, 1)
+    w, e = steady(copy_encode, 5, 1)
     out["rs124_ragged_copy_encode_traffic_GBps"] = round((lay.data_bytes + block.numel()) /
                                                         (e * 1e-3) / 1e9, 1)
     out["rs124_ragged_copy_encode_ms"] = round(e, 3)
