@@ -73,11 +73,11 @@ def settle(fn, seconds: float):
 
 
 def steady(fn, steps: int, warmup: int, seconds: float = 0.3):
-    """timed() after ``seconds`` of back-to-back calls (settle): the batched
-    configurations start right after seconds of host-side data generation,
-    and without it their first timed launches run on a GPU still raising its
-    clocks (config 5's encode ran 4.59 ms at the start of a 10-launch window
-    and 4.14 at its end)."""
+    """timed() after ``seconds`` of back-to-back calls (settle).  The
+    configurations after the headline start right after host-side work (data
+    generation, uploads, checks); without the settle their first timed
+    launches run on a GPU still raising its clocks (config 5's encode ran
+    4.59 ms at the start of a 10-launch window and 4.14 at its end)."""
     settle(fn, seconds)
     return timed(fn, steps, warmup)
 
@@ -1039,8 +1039,8 @@ def main() -> int:
     surv, rows = pkg.decode_matrix(coeff, lost)
     survivors = [codeword[s] for s in surv]
     recovered = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in lost]
-    dwall, dev_ms = timed(lambda: pkg.matvec(rows, survivors, out=recovered, what="ec_rs_decode"),
-                          max(1, args.steps // 2), max(1, args.warmup // 2))
+    dwall, dev_ms = steady(lambda: pkg.matvec(rows, survivors, out=recovered, what="ec_rs_decode"),
+                           max(1, args.steps // 2), max(1, args.warmup // 2))
     torch.cuda.synchronize()
     if not all(torch.equal(r, codeword[g]) for r, g in zip(recovered, lost)):
         raise AssertionError("decode did not reproduce the lost shards")
@@ -1056,7 +1056,7 @@ def main() -> int:
     xh = synth.xor_shards(args.seed, 64 * MiB, 4)
     xd = [torch.from_numpy(h).to(dev) for h in xh]
     xp = torch.empty(64 * MiB, dtype=torch.uint8, device=dev)
-    xwall, xev = timed(lambda: pkg.xor_encode(xd, out=xp), args.steps, args.warmup)
+    xwall, xev = steady(lambda: pkg.xor_encode(xd, out=xp), args.steps, args.warmup)
     # Product-only check: XOR of the parity with the first k-1 shards gives back the last.
     back = pkg.xor_encode(xd[:3] + [xp])
     torch.cuda.synchronize()
