@@ -1,0 +1,31 @@
+"""bench.py's command line, on the CPU: the driver's contract that a run on
+more than one GPU exits with a message (this build measures one GPU), and
+that the options and modes parse.  Neither touches a GPU: the GPU count is
+checked before torch is imported."""
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BENCH = os.path.join(ROOT, "bench.py")
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, BENCH, *args], capture_output=True, text=True,
+                          timeout=120, cwd=ROOT)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = _run("--gpus", "2", "--steps", "3", "--warmup", "1")
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and "--gpus 2" in r.stderr
+    assert r.stdout == ""   # no JSON line for a run that did not happen
+
+
+def test_help_lists_the_modes():
+    r = _run("--help")
+    assert r.returncode == 0
+    for mode in ("full", "headline", "batched-kernels", "batched-pmc", "layout", "small-shards"):
+        assert mode in r.stdout, mode
+    for opt in ("--gpus", "--steps", "--warmup", "--settle-ms"):
+        assert opt in r.stdout, opt
