@@ -213,6 +213,99 @@ def cpu_batched(coeff, hptr, hlen, stripes, unit: int, gpu_parity, seconds: floa
     return res
 
 
+def cpu_update(lay, changed, host_old, hptr, hlen, par_before, gpu_par, seconds: float) -> dict:
+    """The repo's SIMD CPU update (ecfast_parity_update) of config 5's 1 %
+    perturbation: every changed stripe, over host descriptors of the new
+    bytes (the perturbed host copies), the old bytes (``host_old``, one array
+    per changed unit) and a host copy of the parity before the update
+    (``par_before``); gated byte for byte against the GPU's updated parity of
+    those stripes.  GB/s of changed data and ms per update."""
+    import numpy as np
+    import torch
+    import oracle
+    k, m, unit = lay.k, lay.m, lay.unit_bytes
+    stripe = changed // k
+    st, inv = np.unique(stripe, return_inverse=True)
+    nptr = np.zeros((st.size, k), np.uint64)
+    optr = np.zeros((st.size, k), np.uint64)
+    dl = np.zeros((st.size, k), np.uint32)
+    for n, (r, j) in enumerate(zip(inv, changed % k)):
+        nptr[r, j] = hptr[stripe[n], j]
+        optr[r, j] = host_old[n].ctypes.data
+        dl[r, j] = hlen[stripe[n], j]
+    par = np.ascontiguousarray(par_before[st])
+    pp = (np.uint64(par.ctypes.data) +
+          np.arange(st.size * m, dtype=np.uint64).reshape(st.size, m) * np.uint64(unit))
+    oracle.fast_parity_update(lay.coeff, nptr, optr, dl, pp, unit, nthreads=cpu_cores())
+    idx = torch.as_tensor(st.astype(np.int64), device=gpu_par.device)
+    if not np.array_equal(par, gpu_par[idx].cpu().numpy()):
+        raise AssertionError("config 5 update: GPU parity differs from the CPU update")
+    changed_bytes = int(dl.sum())
+    # each further run folds the same delta in again (timing only)
+    res = cpu_rates(lambda t: oracle.fast_parity_update(lay.coeff, nptr, optr, dl, pp, unit,
+                                                        nthreads=t), changed_bytes, seconds)
+    res["all_cores_ms"] = round(changed_bytes / (res["all_cores_GBps"] * 1e9) * 1e3, 3)
+    res["one_core_ms"] = round(changed_bytes / (res["one_core_GBps"] * 1e9) * 1e3, 3)
+    res["sample"] = (f"the whole update: {changed.size} changed units in {st.size} stripes "
+                     f"({changed_bytes / 1e6:.0f} MB of changed data; GB/s of changed data), "
+                     "byte-identical to the GPU's updated parity")
+    return res
+
+
+def cpu_decode_batched(lay, views, lost, hptr, hlen, stripes, gpu_parity,
+                       seconds: float) -> dict:
+    """The repo's SIMD CPU encoder used as a decoder on sampled stripes of
+    config 5: the lost positions rebuilt with the decode rows from the k
+    survivors (data units through host descriptors of the host copies,
+    parity units from a host copy of the GPU's parity of those stripes,
+    ``gpu_parity``: [len(stripes), m, unit]); gated byte for byte against the
+    host copies of the units (``views``, zero-padded past a short unit's
+    end) and the parity.  GB/s of
+    data of the sampled stripes, as the GPU's decode rate is quoted."""
+    import numpy as np
+    import oracle
+    k, m, unit = lay.k, lay.m, lay.unit_bytes
+    surv, rows = oracle.decode_matrix(lay.coeff, k, m, lost)
+    ns = len(stripes)
+    dp = np.ascontiguousarray(hptr[stripes])
+    dl = np.ascontiguousarray(hlen[stripes])
+    gp = np.ascontiguousarray(gpu_parity)
+    sp = np.zeros((ns, k), np.uint64)
+    sl = np.zeros((ns, k), np.uint32)
+    for t, g in enumerate(surv):
+        if g < k:
+            sp[:, t], sl[:, t] = dp[:, g], dl[:, g]
+        else:
+            sp[:, t] = (np.uint64(gp.ctypes.data) + np.arange(ns, dtype=np.uint64)
+                        * np.uint64(m * unit) + np.uint64((g - k) * unit))
+            sl[:, t] = unit
+    e = len(lost)
+    out = np.empty((ns, e, unit), np.uint8)
+    op = (np.uint64(out.ctypes.data) +
+          np.arange(ns * e, dtype=np.uint64).reshape(ns, e) * np.uint64(unit))
+    run = lambda threads: oracle.fast_encode_batched(rows, sp, sl, op, unit, nthreads=threads)
+    run(cpu_cores())
+    for r, g in enumerate(lost):
+        if g >= k:
+            ok = np.array_equal(out[:, r], gp[:, g - k])
+        else:
+            ok = True
+            for n, s in enumerate(stripes):
+                want = np.zeros(unit, np.uint8)
+                u = s * k + g
+                if u < lay.n_units:
+                    t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+                    piece = views[t][i * unit: (i + 1) * unit]
+                    want[: piece.size] = piece
+                ok &= np.array_equal(out[n, r], want)
+        if not ok:
+            raise AssertionError(f"config 5 CPU decode does not rebuild position {g}")
+    res = cpu_rates(run, int(dl.sum()), seconds)
+    res["sample"] = (f"lost {list(lost)}: {ns} stripes ({int(dl.sum()) / 1e6:.0f} MB of data), "
+                     "rebuilding the lost units and parity byte for byte")
+    return res
+
+
 def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: float = 0.0,
                     with_checkpoint: bool = True) -> dict:
     """Configs 4 and 5 through the batched stripe launcher: data GB/s of one
@@ -265,28 +358,34 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     lay = pkg.StripeLayout(tensors, 12, 4, 64 << 10)
     par = lay.alloc_parity()
     w, e = steady(lambda: lay.encode(par), 10, 2)
+    U5 = 64 << 10
+    _, hptr, hlen = stripe_descriptors([v.ctypes.data for v in views],
+                                       [v.size for v in views], 12, U5)
+    sample = list(range(0, lay.n_stripes, max(1, lay.n_stripes // 2000)))
     if cpu_seconds:
-        _, hptr, hlen = stripe_descriptors([v.ctypes.data for v in views],
-                                           [v.size for v in views], 12, 64 << 10)
-        sample = list(range(0, lay.n_stripes, max(1, lay.n_stripes // 2000)))
-        cpu["rs124_ragged"] = {**cpu_batched(lay.coeff, hptr, hlen, sample, 64 << 10,
+        cpu["rs124_ragged"] = {**cpu_batched(lay.coeff, hptr, hlen, sample, U5,
                                              par[sample].cpu().numpy(), cpu_seconds,
                                              "config 5"),
                                "gpu_GBps": round(lay.data_bytes / (w * 1e-3) / 1e9, 1)}
         log(f"config 5 CPU: {cpu['rs124_ragged']}")
-    del views
     out["rs124_ragged_GBps"] = round(lay.data_bytes / (w * 1e-3) / 1e9, 1)
     out["rs124_ragged_traffic_GBps"] = round((lay.data_bytes + par.numel()) / (e * 1e-3) / 1e9, 1)
     out["rs124_ragged_data_GB"] = round(lay.data_bytes / 1e9, 2)
     log(f"config 5 RS(12,4) {lay.n_units} units: {out['rs124_ragged_GBps']} GB/s data")
+    # The seeded 1 % perturbation: new bytes from seeded numpy, written to the
+    # device tensors and to the host copies (the old bytes kept on both sides).
     changed = synth.perturbed_units(seed, lay.n_units, 0.01)
-    olds = []
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
-    for u in changed.tolist():
+    fresh_bytes = synth.perturbation_bytes(seed, lay.host_len.reshape(-1)[changed])
+    par_before = par.cpu().numpy() if cpu_seconds else None
+    olds, host_old = [], []
+    for u, nb in zip(changed.tolist(), fresh_bytes):
         v = lay.unit_view(u)
         olds.append(v.clone())
-        v.copy_(torch.randint(0, 256, (v.numel(),), dtype=torch.uint8, device=dev, generator=g))
+        v.copy_(torch.from_numpy(nb))
+        t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+        hv = views[t][i * U5: i * U5 + nb.size]
+        host_old.append(hv.copy())
+        hv[:] = nb
     plan = lay.plan_update(par, changed, olds)
     lay.run(plan)
     fresh = lay.encode()
@@ -294,25 +393,38 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     if not torch.equal(par, fresh):
         raise AssertionError("incremental update differs from a full re-encode")
     del fresh
+    if cpu_seconds:
+        cpu["rs124_update_1pct"] = cpu_update(lay, changed, host_old, hptr, hlen, par_before,
+                                              par, cpu_seconds)
+        log(f"config 5 update CPU: {cpu['rs124_update_1pct']}")
+    del par_before, host_old
     # each further run folds the same delta in again (timing only)
     w, e = steady(lambda: lay.run(plan), 10, 2)
     changed_bytes = int(lay.host_len.reshape(-1)[changed].sum())
-    upd_traffic = 2 * changed_bytes + 2 * plan.n_stripes * 4 * (64 << 10)
+    upd_traffic = 2 * changed_bytes + 2 * plan.n_stripes * 4 * U5
     out["update_1pct_changed_GB"] = round(changed_bytes / 1e9, 3)
     out["update_1pct_ms"] = round(e, 3)
     out["update_1pct_traffic_GBps"] = round(upd_traffic / (e * 1e-3) / 1e9, 1)
+    if "rs124_update_1pct" in cpu:
+        cpu["rs124_update_1pct"]["gpu_ms"] = out["update_1pct_ms"]
     lay.encode(par)  # repeated update runs toggled the parity; restore it
     lost = [1, 7, 12, 14]
     dplan = lay.plan_decode(par, lost)
     w, e = steady(lambda: lay.run(dplan), 5, 1)
-    k5, S5, U5 = 12, lay.n_stripes, 64 << 10
+    k5, S5 = 12, lay.n_stripes
     surv = [p for p in range(16) if p not in lost][:k5]
     hl = lay.host_len.astype(np.int64)
     dec_traffic = sum(int(hl[:, p].sum()) if p < k5 else S5 * U5 for p in surv + lost)
     out["rs124_ragged_decode4_GBps"] = round(lay.data_bytes / (e * 1e-3) / 1e9, 1)
     out["rs124_ragged_decode4_traffic_GBps"] = round(dec_traffic / (e * 1e-3) / 1e9, 1)
     log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
-    del olds, plan, dplan
+    if cpu_seconds:
+        cpu["rs124_ragged_decode4"] = {
+            **cpu_decode_batched(lay, views, lost, hptr, hlen, sample,
+                                 par[sample].cpu().numpy(), cpu_seconds),
+            "gpu_GBps": out["rs124_ragged_decode4_GBps"]}
+        log(f"config 5 decode CPU: {cpu['rs124_ragged_decode4']}")
+    del views, hptr, hlen, olds, plan, dplan
     # the snapshot's kernel: encode plus a zero-padded copy of every data
     # unit into one stripe-major (stripes, 16, 64 KiB) block, one pass over
     # the data

@@ -98,6 +98,15 @@ def perturbed_units(seed: int, n_units: int, fraction: float = 0.01) -> np.ndarr
     return np.sort(rng.choice(n_units, n, replace=False))
 
 
+def perturbation_bytes(seed: int, lengths) -> List[np.ndarray]:
+    """The new bytes of a seeded perturbation: one uint8 array of lengths[n]
+    uniform random bytes per changed unit n, drawn in one piece from
+    default_rng([seed, 1]) (a stream apart from perturbed_units')."""
+    lengths = np.asarray(lengths, np.int64).reshape(-1)
+    flat = np.random.default_rng([seed, 1]).integers(0, 256, int(lengths.sum()), dtype=np.uint8)
+    return np.split(flat, np.cumsum(lengths)[:-1])
+
+
 # ------------------------------------------------- multi-GB host buffers --
 
 GEN_CHUNK = 64 * MiB  # bytes per independently seeded chunk

@@ -66,6 +66,10 @@ def lib() -> ctypes.CDLL:
         L.ecfast_encode_batched.argtypes = [_u8p, ctypes.c_int, ctypes.c_int, _u64p, _u32p,
                                             _u64p, ctypes.c_uint32, ctypes.c_uint32,
                                             ctypes.c_int]
+        L.ecfast_parity_update.restype = ctypes.c_int
+        L.ecfast_parity_update.argtypes = [_u8p, ctypes.c_int, ctypes.c_int, _u64p, _u64p,
+                                           _u32p, _u64p, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_int]
         _lib = L
     return _lib
 
@@ -245,3 +249,25 @@ def fast_encode_batched(coeff, dptr: np.ndarray, dlen: np.ndarray, pptr: np.ndar
                                    dlen.ctypes.data_as(_u32p), pptr.ctypes.data_as(_u64p),
                                    ns, unit_bytes, nthreads) != 0:
         raise MemoryError("ecfast_encode_batched failed")
+
+
+def fast_parity_update(coeff, nptr: np.ndarray, optr: np.ndarray, dlen: np.ndarray,
+                       pptr: np.ndarray, unit_bytes: int, nthreads: int = 1) -> None:
+    """ecfast_parity_update over descriptor arrays of host addresses: nptr /
+    optr / dlen [n_stripes, k] (nptr 0 = unchanged unit), pptr [n_stripes, m];
+    the parity units are updated in place.  The caller keeps the memory they
+    point at alive."""
+    coeff = np.ascontiguousarray(coeff, np.uint8)
+    m, k = coeff.shape
+    nptr = np.ascontiguousarray(nptr, np.uint64)
+    optr = np.ascontiguousarray(optr, np.uint64)
+    dlen = np.ascontiguousarray(dlen, np.uint32)
+    pptr = np.ascontiguousarray(pptr, np.uint64)
+    ns = nptr.shape[0]
+    if (nptr.shape != (ns, k) or optr.shape != (ns, k) or dlen.shape != (ns, k)
+            or pptr.shape != (ns, m)):
+        raise ValueError("descriptor shapes do not match (n_stripes, k) / (n_stripes, m)")
+    if lib().ecfast_parity_update(_u8(coeff), k, m, nptr.ctypes.data_as(_u64p),
+                                  optr.ctypes.data_as(_u64p), dlen.ctypes.data_as(_u32p),
+                                  pptr.ctypes.data_as(_u64p), ns, unit_bytes, nthreads) != 0:
+        raise MemoryError("ecfast_parity_update failed")

@@ -90,6 +90,7 @@ typedef struct {
   const coef_tab* tabs; /* m*k, row-major; NULL for XOR */
   int k, m;
   uint64_t lo, hi;
+  int accum; /* 1: parity ^= product (the incremental update), 0: parity = product */
 } job;
 
 static void rs_scalar(const job* J, uint64_t lo, uint64_t hi) {
@@ -98,7 +99,7 @@ static void rs_scalar(const job* J, uint64_t lo, uint64_t hi) {
     for (uint64_t b = lo; b < hi; ++b) {
       uint8_t acc = 0;
       for (int j = 0; j < J->k; ++j) acc ^= J->tabs[i * J->k + j].full[J->data[j][b]];
-      p[b] = acc;
+      p[b] = J->accum ? (uint8_t)(p[b] ^ acc) : acc;
     }
   }
 }
@@ -122,7 +123,11 @@ __attribute__((target("avx2"))) static void rs_avx2(const job* J, uint64_t lo,
                                                            _mm256_shuffle_epi8(th, xh)));
       }
     }
-    for (int i = 0; i < J->m; ++i) _mm256_storeu_si256((__m256i*)(J->parity[i] + b), acc[i]);
+    for (int i = 0; i < J->m; ++i) {
+      if (J->accum)
+        acc[i] = _mm256_xor_si256(acc[i], _mm256_loadu_si256((const __m256i*)(J->parity[i] + b)));
+      _mm256_storeu_si256((__m256i*)(J->parity[i] + b), acc[i]);
+    }
   }
   if (b < hi) rs_scalar(J, b, hi);
 }
@@ -147,7 +152,11 @@ __attribute__((target("avx512f,avx512bw"))) static void rs_avx512(const job* J,
                                            _mm512_shuffle_epi8(th, xh), 0x96);
       }
     }
-    for (int i = 0; i < J->m; ++i) _mm512_storeu_si512((void*)(J->parity[i] + b), acc[i]);
+    for (int i = 0; i < J->m; ++i) {
+      if (J->accum)
+        acc[i] = _mm512_xor_si512(acc[i], _mm512_loadu_si512((const void*)(J->parity[i] + b)));
+      _mm512_storeu_si512((void*)(J->parity[i] + b), acc[i]);
+    }
   }
   if (b < hi) rs_scalar(J, b, hi);
 }
@@ -166,7 +175,11 @@ __attribute__((target("avx512f,avx512bw,gfni"))) static void rs_gfni512(const jo
         acc[i] = _mm512_xor_si512(acc[i], _mm512_gf2p8affine_epi64_epi8(x, a, 0));
       }
     }
-    for (int i = 0; i < J->m; ++i) _mm512_storeu_si512((void*)(J->parity[i] + b), acc[i]);
+    for (int i = 0; i < J->m; ++i) {
+      if (J->accum)
+        acc[i] = _mm512_xor_si512(acc[i], _mm512_loadu_si512((const void*)(J->parity[i] + b)));
+      _mm512_storeu_si512((void*)(J->parity[i] + b), acc[i]);
+    }
   }
   if (b < hi) rs_scalar(J, b, hi);
 }
@@ -262,7 +275,7 @@ static void run_threads(job base, uint64_t n, int nthreads) {
 void ecfast_xor_encode(const uint8_t* const* data, int k, uint8_t* parity,
                        uint64_t n, int nthreads) {
   uint8_t* const par[1] = {parity};
-  job base = {data, par, NULL, k, 1, 0, 0};
+  job base = {data, par, NULL, k, 1, 0, 0, 0};
   run_threads(base, n, nthreads);
 }
 
@@ -274,7 +287,7 @@ void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
   const size_t bytes = (sizeof(coef_tab) * (size_t)(k * m) + 63) & ~(size_t)63;
   coef_tab* tabs = (coef_tab*)aligned_alloc(64, bytes);
   for (int i = 0; i < m * k; ++i) make_tab(coeff[i], &tabs[i]);
-  job base = {data, parity, tabs, k, m, 0, 0};
+  job base = {data, parity, tabs, k, m, 0, 0, 0};
   run_threads(base, n, nthreads);
   free(tabs);
 }
@@ -282,14 +295,33 @@ void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
 /* ---- batched stripes (configs 4 and 5) -------------------------------- */
 
 typedef struct {
-  const uint64_t* dptr; /* [S][k], 0 = absent */
+  const uint64_t* dptr; /* [S][k], 0 = absent (update: the new bytes, 0 = unchanged) */
   const uint32_t* dlen; /* [S][k] valid bytes */
   const uint64_t* pptr; /* [S][m] */
   const coef_tab* tabs;
   int k, m;
   uint32_t unit_bytes;
-  uint32_t s_lo, s_hi; /* stripes of this thread */
+  uint32_t s_lo, s_hi;  /* stripes of this thread */
+  const uint64_t* optr; /* update: [S][k] the old bytes; NULL for the encode */
 } bjob;
+
+/* d[b] = a[b] ^ b_[b] for b < n (any alignment). */
+__attribute__((target("avx512f"))) static void xor_bytes_avx512(uint8_t* d, const uint8_t* a,
+                                                                const uint8_t* b_, uint32_t n) {
+  uint32_t b = 0;
+  for (; b + 64 <= n; b += 64)
+    _mm512_storeu_si512((void*)(d + b), _mm512_xor_si512(_mm512_loadu_si512((const void*)(a + b)),
+                                                         _mm512_loadu_si512((const void*)(b_ + b))));
+  for (; b < n; ++b) d[b] = a[b] ^ b_[b];
+}
+
+static void xor_bytes(uint8_t* d, const uint8_t* a, const uint8_t* b_, uint32_t n) {
+  if (isa() >= ISA_AVX512) {
+    xor_bytes_avx512(d, a, b_, n);
+    return;
+  }
+  for (uint32_t b = 0; b < n; ++b) d[b] = a[b] ^ b_[b];
+}
 
 /* Stripes [s_lo, s_hi): units with all unit_bytes valid are read in place;
  * a short or absent unit is copied, zero-padded, into this thread's
@@ -318,23 +350,73 @@ static void* bthread_main(void* arg) {
     }
     for (int i = 0; i < B->m; ++i)
       par[i] = (uint8_t*)(uintptr_t)B->pptr[(uint64_t)s * B->m + i];
-    job J = {data, par, B->tabs, B->k, B->m, 0, U};
+    job J = {data, par, B->tabs, B->k, B->m, 0, U, 0};
     thread_main(&J);
   }
   free(scratch);
   return NULL;
 }
 
-int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* data_ptrs,
-                          const uint32_t* data_len, const uint64_t* parity_ptrs,
-                          uint32_t n_stripes, uint32_t unit_bytes, int nthreads) {
-  if (k < 1 || k > 64 || m < 1 || m > EC_ORACLE_MAX_M) return -1;
+/* Stripes of the incremental update: for each changed unit j of stripe s
+ * (new_ptrs[s][j] != 0) delta_j = new_j ^ old_j over its valid bytes, then
+ * parity_i ^= XOR_j C[i][j] * delta_j over the longest changed unit's bytes,
+ * through the encode kernels in accumulate mode with the coefficient columns
+ * of the changed units only (bytes past a unit's length have a zero delta;
+ * parity bytes past the longest changed unit are unchanged). */
+static void* uthread_main(void* arg) {
+  const bjob* B = (const bjob*)arg;
+  const uint32_t U = B->unit_bytes;
+  uint8_t* scratch = NULL;
+  const uint8_t* delta[64];
+  uint8_t* par[EC_ORACLE_MAX_M];
+  coef_tab* sub = NULL;
+  for (uint32_t s = B->s_lo; s < B->s_hi; ++s) {
+    int nc = 0;
+    uint32_t lmax = 0;
+    for (int j = 0; j < B->k; ++j) {
+      const uint8_t* nw = (const uint8_t*)(uintptr_t)B->dptr[(uint64_t)s * B->k + j];
+      if (!nw) continue;
+      const uint8_t* od = (const uint8_t*)(uintptr_t)B->optr[(uint64_t)s * B->k + j];
+      uint32_t len = B->dlen[(uint64_t)s * B->k + j];
+      if (len > U) len = U;
+      if (!scratch) {
+        scratch = (uint8_t*)malloc((size_t)B->k * U);
+        sub = (coef_tab*)malloc(sizeof(coef_tab) * (size_t)(B->k * B->m));
+        if (!scratch || !sub) {
+          free(scratch);
+          free(sub);
+          return (void*)1;
+        }
+      }
+      uint8_t* d = scratch + (size_t)nc * U;
+      xor_bytes(d, nw, od, len);
+      memset(d + len, 0, U - len);
+      delta[nc] = d;
+      for (int i = 0; i < B->m; ++i) sub[i * B->k + nc] = B->tabs[i * B->k + j];
+      lmax = len > lmax ? len : lmax;
+      ++nc;
+    }
+    if (nc == 0 || lmax == 0) continue;
+    /* sub holds the changed columns at row stride k; compact it to stride nc
+     * (the layout the kernels read) */
+    for (int i = 1; i < B->m; ++i)
+      memmove(&sub[i * nc], &sub[i * B->k], sizeof(coef_tab) * (size_t)nc);
+    for (int i = 0; i < B->m; ++i)
+      par[i] = (uint8_t*)(uintptr_t)B->pptr[(uint64_t)s * B->m + i];
+    job J = {delta, par, sub, nc, B->m, 0, lmax, 1};
+    thread_main(&J);
+  }
+  free(scratch);
+  free(sub);
+  return NULL;
+}
+
+/* Whole stripes per thread: n_stripes split into nthreads contiguous shares,
+ * the calling thread taking the last one.  0, or -1 when a thread failed. */
+static int run_stripe_threads(bjob base, uint32_t n_stripes, int nthreads,
+                              void* (*fn)(void*)) {
   if (nthreads < 1) nthreads = 1;
   if ((uint32_t)nthreads > n_stripes) nthreads = n_stripes ? (int)n_stripes : 1;
-  const size_t bytes = (sizeof(coef_tab) * (size_t)(k * m) + 63) & ~(size_t)63;
-  coef_tab* tabs = (coef_tab*)aligned_alloc(64, bytes);
-  if (!tabs) return -1;
-  for (int i = 0; i < m * k; ++i) make_tab(coeff[i], &tabs[i]);
   pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
   char* created = (char*)calloc((size_t)nthreads, 1);
   bjob* jobs = (bjob*)calloc((size_t)nthreads, sizeof(bjob));
@@ -343,12 +425,12 @@ int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* da
   uint32_t s0 = 0;
   for (int t = 0; status == 0 && t < nthreads; ++t) {
     const uint32_t cnt = per + ((uint32_t)t < extra ? 1u : 0u);
-    bjob b = {data_ptrs, data_len, parity_ptrs, tabs, k, m, unit_bytes, s0, s0 + cnt};
-    jobs[t] = b;
+    jobs[t] = base;
+    jobs[t].s_lo = s0;
+    jobs[t].s_hi = s0 + cnt;
     s0 += cnt;
-    /* The calling thread takes the last share itself. */
-    if (t == nthreads - 1 || pthread_create(&th[t], NULL, bthread_main, &jobs[t]) != 0) {
-      if (bthread_main(&jobs[t]) != NULL) status = -1;
+    if (t == nthreads - 1 || pthread_create(&th[t], NULL, fn, &jobs[t]) != 0) {
+      if (fn(&jobs[t]) != NULL) status = -1;
     } else {
       created[t] = 1;
     }
@@ -360,6 +442,38 @@ int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* da
   free(th);
   free(created);
   free(jobs);
+  return status;
+}
+
+static coef_tab* make_tabs(const uint8_t* coeff, int k, int m) {
+  const size_t bytes = (sizeof(coef_tab) * (size_t)(k * m) + 63) & ~(size_t)63;
+  coef_tab* tabs = (coef_tab*)aligned_alloc(64, bytes);
+  if (tabs)
+    for (int i = 0; i < m * k; ++i) make_tab(coeff[i], &tabs[i]);
+  return tabs;
+}
+
+int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* data_ptrs,
+                          const uint32_t* data_len, const uint64_t* parity_ptrs,
+                          uint32_t n_stripes, uint32_t unit_bytes, int nthreads) {
+  if (k < 1 || k > 64 || m < 1 || m > EC_ORACLE_MAX_M) return -1;
+  coef_tab* tabs = make_tabs(coeff, k, m);
+  if (!tabs) return -1;
+  bjob b = {data_ptrs, data_len, parity_ptrs, tabs, k, m, unit_bytes, 0, 0, NULL};
+  const int status = run_stripe_threads(b, n_stripes, nthreads, bthread_main);
+  free(tabs);
+  return status;
+}
+
+int ecfast_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* new_ptrs,
+                         const uint64_t* old_ptrs, const uint32_t* len,
+                         const uint64_t* parity_ptrs, uint32_t n_stripes, uint32_t unit_bytes,
+                         int nthreads) {
+  if (k < 1 || k > 64 || m < 1 || m > EC_ORACLE_MAX_M || !old_ptrs) return -1;
+  coef_tab* tabs = make_tabs(coeff, k, m);
+  if (!tabs) return -1;
+  bjob b = {new_ptrs, len, parity_ptrs, tabs, k, m, unit_bytes, 0, 0, old_ptrs};
+  const int status = run_stripe_threads(b, n_stripes, nthreads, uthread_main);
   free(tabs);
   return status;
 }

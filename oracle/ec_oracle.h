@@ -69,6 +69,12 @@ void ecfast_rs_encode(const uint8_t* coeff, int k, int m,
 int ecfast_encode_batched(const uint8_t* coeff, int k, int m, const uint64_t* data_ptrs,
                           const uint32_t* data_len, const uint64_t* parity_ptrs,
                           uint32_t n_stripes, uint32_t unit_bytes, int nthreads);
+/* ecref_parity_update's stripes on nthreads threads (whole stripes per
+ * thread); 0, or -1 for bad arguments or out of memory */
+int ecfast_parity_update(const uint8_t* coeff, int k, int m, const uint64_t* new_ptrs,
+                         const uint64_t* old_ptrs, const uint32_t* len,
+                         const uint64_t* parity_ptrs, uint32_t n_stripes, uint32_t unit_bytes,
+                         int nthreads);
 /* force an ISA ("gfni512", "avx512", "avx2", "scalar"); 0 if unsupported */
 int ecfast_force_isa(const char* name);
 

@@ -115,7 +115,8 @@ int main(void) {
     }
     for (int q = 0; q < S * M; ++q) pp[q] = (uint64_t)(uintptr_t)(par + (size_t)q * U);
     ecref_encode_batched(coeff, K, M, dp, ln, pp, S, U);
-    uint8_t old[U];
+    uint8_t old[U], par0[S * M * U];
+    memcpy(par0, par, sizeof par);
     memcpy(old, u[1], ln[1]);
     for (uint32_t b = 0; b < ln[1]; ++b) u[1][b] ^= r8();
     np[1] = dp[1];
@@ -133,6 +134,10 @@ int main(void) {
       for (int q = 0; q < S * M; ++q) pp3[q] = (uint64_t)(uintptr_t)(par3 + (size_t)q * U);
       if (ecfast_encode_batched(coeff, K, M, dp, ln, pp3, S, U, th) != 0) FAIL("fast batched");
       if (memcmp(par3, par, sizeof par)) FAIL("fast batched differs (%d threads)", th);
+      /* the SIMD update from the parity before the change */
+      memcpy(par3, par0, sizeof par3);
+      if (ecfast_parity_update(coeff, K, M, np, op, ln, pp3, S, U, th) != 0) FAIL("fast update");
+      if (memcmp(par3, par, sizeof par)) FAIL("fast update differs (%d threads)", th);
     }
     for (int q = 0; q < S * K; ++q) free(u[q]);
   }

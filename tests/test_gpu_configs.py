@@ -6,8 +6,10 @@ Every output is compared byte for byte against the CPU encoder
 (oracle/ec_cpu_fast.c, itself pinned to the scalar oracle by test_oracle.py)
 on the same seeded numpy bytes: configs 1 and 2 whole, configs 4 and 5 stripe
 by stripe over the whole buffer, the config-3 decode against the original
-shards.  On top, size-independent properties over the whole buffer: erase ->
-decode round trips and update == full re-encode.
+shards, config 5's incremental update (seeded numpy bytes) stripe by stripe
+against the CPU encoder over the perturbed bytes.  On top, size-independent
+properties over the whole buffer: erase -> decode round trips and update ==
+full re-encode.
 """
 import os
 
@@ -145,20 +147,28 @@ def test_config5_ragged_3000_rs124_and_update(pkg, dev, synth):
     _say(f"config 5: {lay.data_bytes / 1e9:.2f} GB in {lay.n_units} units, {lay.n_stripes} stripes")
     torch.cuda.synchronize()
     _check_every_stripe(lay, pset.parity, views, "config 5")
-    del block, views
     rng = np.random.default_rng(5)
-    # Incremental update after a seeded 1% perturbation == full re-encode.
+    # Incremental update after a seeded 1% perturbation: the new bytes come
+    # from seeded numpy, go to the device tensors and to the host copies, and
+    # the updated parity of every stripe is compared with the CPU encoder
+    # over the perturbed host bytes.
     changed = synth.perturbed_units(5, lay.n_units, 0.01)
+    unit = lay.unit_bytes
+    fresh_bytes = synth.perturbation_bytes(5, lay.host_len.reshape(-1)[changed])
     olds = []
-    for u in changed.tolist():
+    for u, nb in zip(changed.tolist(), fresh_bytes):
         v = lay.unit_view(u)
         olds.append(v.clone())
-        v.copy_(torch.randint(0, 256, (v.numel(),), dtype=torch.uint8, device=dev))
+        v.copy_(torch.from_numpy(nb))
+        t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+        views[t][i * unit: i * unit + nb.size] = nb
     pkg.update(pset, changed, olds)
+    torch.cuda.synchronize()
+    _check_every_stripe(lay, pset.parity, views, f"config 5 after the update of {changed.size} units")
     fresh = lay.encode()
     torch.cuda.synchronize()
     assert torch.equal(pset.parity, fresh)
-    _say(f"config 5: update of {changed.size} units == re-encode")
+    del block, views, fresh, olds
     # Round trip: lose 4 positions (2 data, 2 parity) of every stripe.
     lost = sorted(rng.choice(12, 2, replace=False).tolist() + (12 + rng.choice(4, 2, replace=False)).tolist())
     refs = [t.clone() for t in tensors]

@@ -215,6 +215,43 @@ def test_golden_rs(pkg, dev, name):
 
 # ---------------------------------------------------------------- batched --
 
+@pytest.mark.parametrize("arena", [False, True])
+def test_golden_ragged_encode_and_update(pkg, dev, arena):
+    """The committed ragged fixture (RS(12,4), 256-byte units over 24 tensors,
+    written by the pure-Python restatement): the batched encode equals its
+    ``parity``, and the incremental update of its ``changed`` units to the
+    bytes of ``new`` equals its ``parity_after``.  The tensors are separate
+    allocations, or (arena) views back to back in one buffer, 4-byte aligned
+    as the fixture's sizes leave them."""
+    g = np.load(os.path.join(GOLDEN, "ragged_12_4.npz"))
+    k, m, unit = int(g["k"]), int(g["m"]), int(g["unit"])
+    sizes = [int(x) for x in g["sizes"]]
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(int)
+    if arena:
+        buf = torch.from_numpy(g["data"]).to(dev)
+        tensors = [buf[o: o + n] for o, n in zip(offs, sizes)]
+    else:
+        tensors = [torch.from_numpy(g["data"][o: o + n]).to(dev) for o, n in zip(offs, sizes)]
+    pset = pkg.encode(tensors, k, m, unit)
+    lay = pset.layout
+    torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(), g["parity"])
+    olds = []
+    for u in g["changed"]:
+        u = int(u)
+        v = lay.unit_view(u)
+        olds.append(v.clone())
+        t, i = int(lay.unit_tensor[u]), int(lay.unit_index[u])
+        start = int(offs[t]) + i * unit
+        v.copy_(torch.from_numpy(g["new"][start: start + v.numel()]))
+    pkg.update(pset, g["changed"], olds)
+    torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(), g["parity_after"])
+    got = np.concatenate([t.cpu().numpy() for t in tensors])
+    assert np.array_equal(got, g["new"])
+
+
+
 def _ragged_device(rng, dev, n_tensors, max_bytes, misalign=False):
     """Device tensors of random byte sizes (some zero-length-free, some odd),
     optionally as views at odd offsets of one arena whose gaps hold 0xC3 (a
@@ -249,6 +286,39 @@ def _oracle_layout_parity(layout, host, unit):
             row.append(host[t][i * unit: (i + 1) * unit])
         grid.append(row)
     return oracle.encode_batched(layout.coeff, grid, layout.host_len, unit)
+
+
+def _perturb_units(rng, layout, host, changed):
+    """New random bytes (seeded numpy) for the changed units, written into
+    the device tensors and into host copies of the tensors.  Returns the
+    device copies of the old bytes (the update's input) and the host copies
+    of the tensors after the change."""
+    unit = layout.unit_bytes
+    host_new = [h.copy() for h in host]
+    olds = []
+    for u in changed:
+        u = int(u)
+        v = layout.unit_view(u)
+        olds.append(v.clone())
+        fresh = rng.integers(0, 256, v.numel(), dtype=np.uint8)
+        v.copy_(torch.from_numpy(fresh))
+        t, i = int(layout.unit_tensor[u]), int(layout.unit_index[u])
+        host_new[t][i * unit: i * unit + fresh.size] = fresh
+    return olds, host_new
+
+
+def _oracle_update(layout, host_old, host_new, changed, par_before):
+    """The oracle's incremental update (ecref_parity_update) of a copy of
+    ``par_before`` over host copies of the changed units' old and new bytes."""
+    k, unit = layout.k, layout.unit_bytes
+    newu = [[None] * k for _ in range(layout.n_stripes)]
+    oldu = [[None] * k for _ in range(layout.n_stripes)]
+    for u in changed:
+        s, j = divmod(int(u), k)
+        t, i = int(layout.unit_tensor[u]), int(layout.unit_index[u])
+        newu[s][j] = host_new[t][i * unit: (i + 1) * unit]
+        oldu[s][j] = host_old[t][i * unit: (i + 1) * unit]
+    return oracle.parity_update(layout.coeff, newu, oldu, layout.host_len, par_before.copy(), unit)
 
 
 @pytest.mark.parametrize("k,m,unit,misalign", [(12, 4, 4096, False), (8, 2, 1024, True),
@@ -500,15 +570,15 @@ def test_batched_update_equals_reencode(pkg, dev, k, m, unit, misalign):
     host, tensors = _ragged_device(rng, dev, 60, 8 * unit, misalign)
     pset = pkg.encode(tensors, k, m, unit)
     lay = pset.layout
+    par0 = _oracle_layout_parity(lay, host, unit)
     changed = np.sort(rng.choice(lay.n_units, max(1, lay.n_units // 10), replace=False))
-    olds = []
-    for u in changed:
-        v = lay.unit_view(int(u))
-        olds.append(v.clone())
-        v.copy_(torch.from_numpy(rng.integers(0, 256, v.numel(), dtype=np.uint8)))
+    olds, host_new = _perturb_units(rng, lay, host, changed)
     pkg.update(pset, changed, olds)
     fresh = lay.encode()
     torch.cuda.synchronize()
+    want = _oracle_update(lay, host, host_new, changed, par0)
+    assert np.array_equal(pset.parity.cpu().numpy(), want)
+    assert np.array_equal(want, _oracle_layout_parity(lay, host_new, unit))
     assert torch.equal(pset.parity, fresh)
 
 
@@ -626,14 +696,13 @@ def test_batched_wide_codes(pkg, dev, k, m, unit, lost):
         assert np.array_equal(t.cpu().numpy(), h)
     assert torch.equal(pset.parity, par_ref)
     changed = np.sort(rng.choice(lay.n_units, max(1, lay.n_units // 7), replace=False))
-    olds = []
-    for u in changed:
-        v = lay.unit_view(int(u))
-        olds.append(v.clone())
-        v.copy_(torch.from_numpy(rng.integers(0, 256, v.numel(), dtype=np.uint8)))
+    par0 = pset.parity.cpu().numpy()   # equal to the oracle's parity (checked above)
+    olds, host_new = _perturb_units(rng, lay, host, changed)
     pkg.update(pset, changed, olds)
     fresh = lay.encode()
     torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(),
+                          _oracle_update(lay, host, host_new, changed, par0))
     assert torch.equal(pset.parity, fresh)
 
 
@@ -985,14 +1054,12 @@ def test_batched_random_layouts(pkg, dev, seed):
     assert torch.equal(pset.parity, par_ref), lost
     # update of random units
     changed = np.sort(r.choice(lay.n_units, max(1, lay.n_units // 4), replace=False))
-    olds = []
-    for u in changed:
-        v = lay.unit_view(int(u))
-        olds.append(v.clone())
-        v.copy_(torch.from_numpy(r.integers(0, 256, v.numel(), dtype=np.uint8)))
+    olds, host_new = _perturb_units(r, lay, host, changed)
     pkg.update(pset, changed, olds)
     fresh = lay.encode()
     torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(),
+                          _oracle_update(lay, host, host_new, changed, want_par)), (k, m, unit)
     assert torch.equal(pset.parity, fresh)
 
 

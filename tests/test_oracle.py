@@ -294,6 +294,47 @@ def test_fast_batched_encoder_matches_oracle(isa):
         oracle.fast_force_isa(default)
 
 
+@pytest.mark.parametrize("isa", ["scalar", "avx2", "avx512", "gfni512"])
+def test_fast_parity_update_matches_oracle(isa):
+    """The SIMD incremental update (the CPU baseline beside the GPU update)
+    equals the scalar oracle's update on ragged stripes with short, absent
+    and unchanged units, for several thread counts, and both equal a fresh
+    encode of the changed bytes."""
+    default = oracle.fast_isa()
+    if not oracle.fast_force_isa(isa):
+        pytest.skip(f"{isa} not supported on this host")
+    try:
+        rng = np.random.default_rng(23)
+        for k, m, unit, threads, frac in [(12, 4, 96, 3, 0.3), (8, 2, 4096, 2, 0.1),
+                                          (6, 3, 64, 1, 1.0), (4, 1, 1024, 7, 0.5),
+                                          (12, 4, 65536, 4, 0.05)]:
+            grid, glen = _ragged(rng, k, unit, 9)
+            C = oracle.cauchy(k, m)
+            par0 = oracle.encode_batched(C, grid, glen, unit)
+            new_grid = [[None if u is None else u.copy() for u in row] for row in grid]
+            ns = len(grid)
+            nptr = np.zeros((ns, k), np.uint64)
+            optr = np.zeros((ns, k), np.uint64)
+            newu = [[None] * k for _ in grid]
+            oldu = [[None] * k for _ in grid]
+            for s, row in enumerate(new_grid):
+                for j, u in enumerate(row):
+                    if u is not None and rng.random() < frac:
+                        oldu[s][j] = grid[s][j]
+                        u[:] = rng.integers(0, 256, u.size, dtype=np.uint8)
+                        newu[s][j] = u
+                        nptr[s, j], optr[s, j] = u.ctypes.data, grid[s][j].ctypes.data
+            want = oracle.parity_update(C, newu, oldu, glen, par0.copy(), unit)
+            got = par0.copy()
+            pptr = np.array([[got[s, i].ctypes.data for i in range(m)] for s in range(ns)],
+                            np.uint64).reshape(ns, m)
+            oracle.fast_parity_update(C, nptr, optr, glen, pptr, unit, nthreads=threads)
+            assert np.array_equal(got, want), (k, m, unit, threads)
+            assert np.array_equal(got, oracle.encode_batched(C, new_grid, glen, unit))
+    finally:
+        oracle.fast_force_isa(default)
+
+
 # ------------------------------------------------------------------ golden --
 
 def _golden(name):
@@ -344,5 +385,15 @@ def test_golden_ragged():
     for u in g["changed"]:
         s, j = divmod(int(u), k)
         newu[s][j], oldu[s][j] = ng[s][j], og[s][j]
+    fast = par.copy()
     oracle.parity_update(C, newu, oldu, glen, par, unit)
     assert np.array_equal(par, g["parity_after"])
+    # the SIMD update over host descriptors of the same bytes
+    nptr = np.array([[0 if u is None else u.ctypes.data for u in row] for row in newu],
+                    np.uint64).reshape(ns, k)
+    optr = np.array([[0 if u is None else u.ctypes.data for u in row] for row in oldu],
+                    np.uint64).reshape(ns, k)
+    pptr = np.array([[fast[s, i].ctypes.data for i in range(m)] for s in range(ns)],
+                    np.uint64).reshape(ns, m)
+    oracle.fast_parity_update(C, nptr, optr, glen, pptr, unit, nthreads=3)
+    assert np.array_equal(fast, g["parity_after"])

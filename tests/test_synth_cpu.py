@@ -61,3 +61,21 @@ def test_ragged_host_independent_of_threads():
     sizes, _ = synth.ragged_sizes(5, 40)
     assert [v.size for v in views1] == sizes.tolist()
     assert all(v.ctypes.data % 64 == 0 for v in views1)
+
+
+def test_perturbation_is_seeded():
+    """The 1 % perturbation: the unit choice and the new bytes are functions
+    of the seed alone (the GPU tests and the bench draw them on the host and
+    upload them, so a CPU re-encode sees the same bytes)."""
+    u1 = synth.perturbed_units(5, 10_000, 0.01)
+    assert u1.size == 100 and np.array_equal(u1, np.unique(u1))
+    assert np.array_equal(u1, synth.perturbed_units(5, 10_000, 0.01))
+    lens = np.array([65536, 17, 0, 4096])
+    a = synth.perturbation_bytes(5, lens)
+    b = synth.perturbation_bytes(5, lens)
+    assert [x.size for x in a] == lens.tolist()
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+    c = synth.perturbation_bytes(6, lens)
+    assert not np.array_equal(a[0], c[0])
+    # roughly uniform bytes
+    assert abs(a[0].mean() - 127.5) < 2
