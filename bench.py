@@ -475,12 +475,14 @@ def checkpoint_staging(pkg, tensors) -> dict:
         t0 = time.perf_counter()
         _, slices = codec.encode(tensors)
         t_cold = time.perf_counter() - t0
+        stats = [codec.last_stage_stats]
         t_enc = []
         for _ in range(3):
             codec.release(slices)            # the next encode writes into the same array
             t0 = time.perf_counter()
             meta, slices = codec.encode(tensors)
             t_enc.append(time.perf_counter() - t0)
+            stats.append(codec.last_stage_stats)
         keep = {p: slices[p] for p in range(16) if p not in (2, 9)}  # lose 2 data slices
         keep = dict(list(sorted(keep.items()))[:12])
         t_dec = []
@@ -497,9 +499,13 @@ def checkpoint_staging(pkg, tensors) -> dict:
         codec.release(slices)
         log(f"staging calls: encode {[round(t, 3) for t in t_enc]} s (cold {t_cold:.3f}), "
             f"decode {[round(t, 3) for t in t_dec]} s")
+        for name, st in zip(["cold", "warm 1", "warm 2", "warm 3"], stats):
+            log(f"staging {name}: {st}")
         res = {"ckpt_encode_to_host_GBps": round(nbytes / statistics.median(t_enc) / 1e9, 1),
                "ckpt_encode_to_host_cold_GBps": round(nbytes / t_cold / 1e9, 1),
-               "ckpt_decode_from_host_GBps": round(nbytes / statistics.median(t_dec) / 1e9, 1)}
+               "ckpt_decode_from_host_GBps": round(nbytes / statistics.median(t_dec) / 1e9, 1),
+               "ckpt_encode_calls_s": [round(t, 3) for t in [t_cold] + t_enc],
+               "ckpt_encode_stage_stats": stats}
     except RuntimeError as e:  # pinned-memory limits differ between hosts
         res = {"ckpt_staging_error": str(e)[:200]}
     log(f"checkpoint staging: {res}")
@@ -1006,45 +1012,6 @@ def training_in_child() -> dict:
         return {"train_error": "timed out"}
 
 
-def gf_variants(pkg, synth, dev, seed: int, steps: int) -> int:
-    """The product's GF(2^8) multiply (v_perm tables, rs_kernel) against the
-    textbook LDS log/exp tables (libec_probe.so's logexp_kernel, same grid,
-    tile order and memory instructions) on config 2's shards: HIP events per
-    launch and a byte comparison of the parity."""
-    import ctypes
-    import torch
-    lib = ctypes.CDLL(os.path.join(ROOT, "probe", "libec_probe.so"))
-    lib.ecp_rs_logexp.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                  ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
-    k, m, shard = 6, 3, 256 * MiB
-    data = [torch.from_numpy(h).to(dev) for h in synth.rs_shards(seed, shard, k)]
-    coeff = pkg.cauchy_matrix(k, m)
-    ref = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
-    alt = [torch.empty(shard, dtype=torch.uint8, device=dev) for _ in range(m)]
-    src = (ctypes.c_void_p * k)(*[t.data_ptr() for t in data])
-    dst = (ctypes.c_void_p * m)(*[t.data_ptr() for t in alt])
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-    def logexp():
-        rc = lib.ecp_rs_logexp(coeff.ctypes.data_as(ctypes.c_void_p), k, m, src, dst, shard, st)
-        if rc != 0:
-            raise RuntimeError(f"ecp_rs_logexp returned {rc}")
-
-    _, vperm_ms = timed(lambda: pkg.matvec(coeff, data, out=ref), steps, 5)
-    _, lds_ms = timed(logexp, steps, 5)
-    torch.cuda.synchronize()
-    if not all(torch.equal(a, b) for a, b in zip(ref, alt)):
-        raise AssertionError("LDS log/exp parity differs from the product's")
-    traffic = (k + m) * shard
-    print(json.dumps({"mode": "gf-variants",
-                      "vperm_rs_kernel_us": round(vperm_ms * 1e3, 2),
-                      "vperm_traffic_GBps": round(traffic / (vperm_ms * 1e-3) / 1e9, 1),
-                      "lds_logexp_kernel_us": round(lds_ms * 1e3, 2),
-                      "lds_logexp_traffic_GBps": round(traffic / (lds_ms * 1e-3) / 1e9, 1),
-                      "parity_equal": True}), flush=True)
-    return 0
-
-
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1060,7 +1027,7 @@ def main() -> int:
                     help="skip the 20.8 GB RS(8,2) and ragged RS(12,4) configurations")
     ap.add_argument("--mode", choices=["full", "headline", "decode", "flat-kernels", "pmc",
                                        "batched", "batched-kernels", "batched-pmc",
-                                       "gf-variants", "train", "small-shards", "layout"],
+                                       "train", "small-shards", "layout"],
                     default="full",
                     help="full: everything (default); headline: only the timed RS(6,3) "
                          "encode (for kernel-trace profiles); flat-kernels: configs 2, 3 "
@@ -1070,8 +1037,7 @@ def main() -> int:
                          "batched: configs 4 and 5 only; batched-kernels: the same without "
                          "the checkpoint staging and snapshot (for kernel-trace profiles); "
                          "batched-pmc: the copy plus 3 launches of each batched kernel, for "
-                         "counter runs; gf-variants: "
-                         "the v_perm GF multiply against LDS log/exp tables; train: a training "
+                         "counter runs; train: a training "
                          "loop with synchronous and with snapshot checkpoint saves; "
                          "small-shards: RS(6,3) over 1 and 4 MiB shards, eager and planned; "
                          "layout: RS(6,3) over config 2's bytes as six shards, cut into "
@@ -1101,8 +1067,6 @@ def main() -> int:
         return 0
     if args.mode == "batched-pmc":
         return batched_pmc_launches(pkg, synth, dev, args.seed)
-    if args.mode == "gf-variants":
-        return gf_variants(pkg, synth, dev, args.seed, min(args.steps, 50))
     if args.mode == "small-shards":
         print(json.dumps({"mode": args.mode, **small_shards(pkg, dev)}), flush=True)
         return 0

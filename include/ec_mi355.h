@@ -33,7 +33,8 @@
  *   - device work is enqueued on `stream` (a hipStream_t; NULL = the legacy
  *     default stream) and is asynchronous with respect to the host;
  *   - calls on different streams from different host threads are safe: the
- *     library keeps no mutable global state.
+ *     library keeps no mutable global state (only each thread's timings of
+ *     its last staging call, ec_stage_last_stats).
  */
 #ifndef EC_MI355_H
 #define EC_MI355_H
@@ -45,7 +46,9 @@
 extern "C" {
 #endif
 
-#define EC_ABI_VERSION 1
+/* 2: ec_stage_stripes_to_host added; the batched kernels read every
+ * descriptor entry of a stripe, also the length of an absent unit. */
+#define EC_ABI_VERSION 2
 
 /* Status codes. */
 #define EC_OK 0
@@ -296,6 +299,25 @@ int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_
 int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row_bytes,
                        uint8_t* d_dst, uint64_t dst_pitch, uint8_t* h_pinned,
                        uint64_t pinned_bytes, int threads, ec_stream_t stream);
+
+/* Timings of a staging call, to tell a slow link from a slow host side. */
+typedef struct {
+  uint32_t chunks;    /* transfers of one pinned half each                   */
+  double wall_s;      /* the whole call                                      */
+  double wait_s;      /* host time blocked until a half's transfers landed   */
+  double host_copy_s; /* host time in the threads' copies (scatter, gather)  */
+  double max_wait_s;  /* the longest single wait                             */
+  double device_s;    /* device time from the first transfer's start to the
+                         last one's end (0 when not measured)                */
+} ec_stage_stats;
+
+/* The timings of the calling thread's last ec_stage_to_host,
+ * ec_stage_stripes_to_host or ec_stage_to_device call that moved bytes
+ * (kept per thread: the one piece of state the library holds).  EC_EINVAL
+ * for a null pointer.  No counterpart in the reference: a diagnostic of the
+ * staging of coded checkpoints (tensor_aware_state_dict.py:245-274 is the
+ * reference's unmeasured D2H). */
+int ec_stage_last_stats(ec_stage_stats* out);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ import threading
 
 LIB_NAME = "libec_mi355.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EC_OK = 0
 EC_EINVAL = -1
@@ -45,7 +45,26 @@ EXPORTS = (
     "ec_stage_to_host",
     "ec_stage_stripes_to_host",
     "ec_stage_to_device",
+    "ec_stage_last_stats",
 )
+
+
+class StageStats(ctypes.Structure):
+    """ec_stage_stats: the timings of a staging call."""
+    _fields_ = [("chunks", ctypes.c_uint32), ("wall_s", ctypes.c_double),
+                ("wait_s", ctypes.c_double), ("host_copy_s", ctypes.c_double),
+                ("max_wait_s", ctypes.c_double), ("device_s", ctypes.c_double)]
+
+    def as_dict(self) -> dict:
+        return {name: round(getattr(self, name), 4) if name != "chunks" else self.chunks
+                for name, _ in self._fields_}
+
+
+def last_stage_stats() -> dict:
+    """ec_stage_last_stats of the calling thread, as a dict."""
+    st = StageStats()
+    check(lib().ec_stage_last_stats(ctypes.byref(st)), "ec_stage_last_stats")
+    return st.as_dict()
 
 
 class ECLibraryMissing(RuntimeError):
@@ -83,6 +102,9 @@ def lib() -> ctypes.CDLL:
     L.ec_abi_version.argtypes = []
     if L.ec_abi_version() != ABI_VERSION:
         raise ECLibraryMissing(f"{LIB_PATH} has ABI {L.ec_abi_version()}, expected {ABI_VERSION}")
+    missing = [name for name in EXPORTS if not hasattr(L, name)]
+    if missing:
+        raise ECLibraryMissing(f"{LIB_PATH} lacks {', '.join(missing)}; rebuild it")
     L.ec_strerror.restype = ctypes.c_char_p
     L.ec_strerror.argtypes = [_i]
     L.ec_gf_mul.restype = ctypes.c_uint8
@@ -119,6 +141,8 @@ def lib() -> ctypes.CDLL:
     L.ec_stage_stripes_to_host.argtypes = [_vp, _u32, _u32, _u64, _vp, _vp, _u64, _i, _vp]
     L.ec_stage_to_device.restype = _i
     L.ec_stage_to_device.argtypes = [_vp, _u32, _u64, _vp, _u64, _vp, _u64, _i, _vp]
+    L.ec_stage_last_stats.restype = _i
+    L.ec_stage_last_stats.argtypes = [ctypes.POINTER(StageStats)]
     _lib = L
     return L
 

@@ -115,15 +115,18 @@ def _dtype(name: str) -> torch.dtype:
 # ----------------------------------------------------------------- codec --
 
 _staging_threads: "weakref.WeakSet[threading.Thread]" = weakref.WeakSet()
-_staging_join_registered = False
 
 
 def _join_staging_threads() -> None:
-    """At interpreter exit: let background staging finish before the hook
-    that waits for the side streams (registered after it, so it runs
-    first)."""
+    """At interpreter exit: let background staging finish (its transfers
+    land and its threads end) before the hook that waits for the engine's
+    streams and devices (codec._finish_side_streams, registered earlier, at
+    that module's import, so it runs after this one)."""
     for t in list(_staging_threads):
         t.join()
+
+
+atexit.register(_join_staging_threads)
 
 
 class PendingSlices:
@@ -147,10 +150,6 @@ class PendingSlices:
             return
         self._thread = threading.Thread(target=self._run, args=(stage,), daemon=True,
                                         name="ec-stage")
-        global _staging_join_registered
-        if not _staging_join_registered:
-            atexit.register(_join_staging_threads)
-            _staging_join_registered = True
         _staging_threads.add(self._thread)
         self._thread.start()
 
@@ -165,6 +164,13 @@ class PendingSlices:
     def done(self) -> bool:
         return self._done.is_set()
 
+    def wait(self) -> None:
+        """Wait until the staging has ended (its transfers have landed or it
+        failed), without raising what it raised."""
+        self._done.wait()
+        if self._thread is not None:
+            self._thread.join()
+
     def result(self, timeout: Optional[float] = None) -> Tuple[dict, List[np.ndarray]]:
         if not self._done.wait(timeout):
             raise TimeoutError("checkpoint slices still being staged")
@@ -173,6 +179,16 @@ class PendingSlices:
         if self._error is not None:
             raise self._error
         return self._result
+
+
+def _lib_call(name: str, coeff: np.ndarray, *args) -> None:
+    """Call the batched entry point ``name`` of the C ABI with a host
+    coefficient matrix first and (stream, device) last."""
+    from . import _lib
+    from .codec import stream_handle
+    *rest, stream, dev = args
+    _lib.check(getattr(_lib.lib(), name)(_lib.u8ptr(np.ascontiguousarray(coeff, np.uint8)), *rest,
+                                         stream_handle(stream, dev)), name)
 
 
 class GpuSliceCodec:
@@ -216,29 +232,38 @@ class GpuSliceCodec:
     slowed the training kernels beside them."""
 
     def __init__(self, k: int, m: int, unit_bytes: int, chunk_bytes: int = 1 << 30,
-                 snapshot_bytes: Optional[int] = None):
+                 snapshot_bytes: Optional[int] = None, keep_block: bool = False):
         from . import layout as _layout
         self._layout = _layout
         self.k, self.m, self.unit_bytes = k, m, unit_bytes
         self.chunk_bytes = chunk_bytes
         self.snapshot_bytes = snapshot_bytes
+        self.keep_block = keep_block
         self.stage_threads = 8   # host threads of the staging calls
         self._free: Optional[np.ndarray] = None   # released by the caller, reusable
         self._host_lock = threading.Lock()
         self._last_layout = None   # descriptors of the last encode, without its tensors
         self._last_ptrs = None     # (block key, parity table, data table) of the last snapshot
+        # keep_block: (block, PendingSlices staging it) of the last save, when
+        # that save coded the whole state into one block (the snapshot path)
+        self._resident: Optional[Tuple[torch.Tensor, "PendingSlices"]] = None
+        # ec_stage_last_stats of the last staging call (a diagnostic: the
+        # transfer waits, host copies and device time of that call)
+        self.last_stage_stats: Optional[dict] = None
 
     def _stripe_layout(self, tensors: List[torch.Tensor]):
-        """The StripeLayout of the tensors to encode.  When they occupy the
-        same device bytes as at the last encode (a training run saves the
-        same buffers every time), its descriptors are reused: no descriptor
-        build and no upload on the path that holds training."""
+        """(layout, reused): the StripeLayout of the tensors to encode, and
+        whether they occupy the same device bytes as at the last encode (a
+        training run saves the same buffers every time).  Then its
+        descriptors are reused: no descriptor build and no upload on the path
+        that holds training."""
         prev = self._last_layout
         lay = prev.rebind(tensors) if prev is not None else None
-        if lay is None:
-            lay = self._layout.StripeLayout(tensors, self.k, self.m, self.unit_bytes)
-            self._last_layout = lay.descriptors_only()
-        return lay
+        if lay is not None:
+            return lay, True
+        lay = self._layout.StripeLayout(tensors, self.k, self.m, self.unit_bytes)
+        self._last_layout = lay.descriptors_only()
+        return lay, False
 
     def _host_out(self, shape: Tuple[int, int]) -> np.ndarray:
         """The released host array when it has this shape, else a new one.
@@ -322,11 +347,13 @@ class GpuSliceCodec:
                 "n_stripes": lay.n_stripes, "n_units": lay.n_units,
                 "tensors": _tensor_meta(tensors), "generator": GENERATOR_ID}
 
-    def encode(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
+    def encode(self, tensors: Sequence[torch.Tensor],
+               changed_tensors: Optional[Sequence[int]] = None) -> Tuple[dict, List[np.ndarray]]:
         """Code the tensors into k + m slices in host memory; returns when
         they are there.  Through one HBM block when it fits (``snapshot``,
-        waited for), else in bounded chunks: the same slices either way."""
-        return self.snapshot(tensors).result()
+        waited for), else in bounded chunks: the same slices either way.
+        ``changed_tensors`` as for ``snapshot``."""
+        return self.snapshot(tensors, changed_tensors=changed_tensors).result()
 
     def _encode_chunked(self, tensors: Sequence[torch.Tensor]) -> Tuple[dict, List[np.ndarray]]:
         """Code and stage in bounded chunks of stripes; returns when the slices
@@ -340,7 +367,7 @@ class GpuSliceCodec:
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
-        lay = self._stripe_layout(tensors)
+        lay, _ = self._stripe_layout(tensors)
         S, dev = lay.n_stripes, lay.device
         C = self._chunk_stripes(S, k + m)
         chunks = [(c0, min(C, S - c0)) for c0 in range(0, S, C)]
@@ -383,7 +410,8 @@ class GpuSliceCodec:
                     "ec_stage_stripes_to_host")
         return self._meta(lay, tensors), [out[p] for p in range(k + m)]
 
-    def snapshot(self, tensors: Sequence[torch.Tensor], hold: bool = True) -> "PendingSlices":
+    def snapshot(self, tensors: Sequence[torch.Tensor], hold: bool = True,
+                 changed_tensors: Optional[Sequence[int]] = None) -> "PendingSlices":
         """Code the tensors into one stripe-major (stripes, k + m, unit_bytes)
         block in HBM and stage it to host memory in the background.
 
@@ -407,14 +435,33 @@ class GpuSliceCodec:
         training steps keep their room) or the allocator cannot provide it,
         the state is coded and staged by ``encode`` before this returns (the
         bounded chunked path: a longer stall, the same slices), and the
-        result is ready at once."""
-        from . import _lib
-        from .codec import side_stream, stream_handle
+        result is ready at once.
+
+        Incremental saves (a codec built with ``keep_block``): the block
+        stays in HBM after staging, holding the last save's data units and
+        parity.  A save that passes ``changed_tensors`` (indices into
+        ``tensors`` of every tensor whose bytes may differ from the last
+        save's) over the same device bytes as the last save (the same
+        addresses and sizes, in order) then codes only those tensors' units:
+        ``ec_parity_update`` folds new XOR old (the block's copy) into the
+        block's parity, and the new units are copied into the block, so it
+        again holds the whole state coded, and is staged as above.  The
+        slices are those a full encode gives, as long as no tensor outside
+        ``changed_tensors`` changed: the caller vouches for that.  Anything
+        else (no block from the last save, other tensors, no
+        ``changed_tensors``) takes the full encode.  The update waits for the
+        last save's staging to finish reading the block."""
+        from .codec import side_stream
         k, m, U = self.k, self.m, self.unit_bytes
         tensors = list(tensors)
-        lay = self._stripe_layout(tensors)
+        lay, reused = self._stripe_layout(tensors)
         S, dev = lay.n_stripes, lay.device
         cur = torch.cuda.current_stream(dev)
+        res, self._resident = self._resident, None
+        if (changed_tensors is not None and self.keep_block and reused and res is not None
+                and tuple(res[0].shape) == (S, k + m, U) and res[0].device == dev):
+            return self._snapshot_delta(lay, tensors, res, changed_tensors, hold)
+        del res
         block = None
         if (k + m) * S * U <= self._snapshot_limit(dev):
             try:
@@ -432,10 +479,20 @@ class GpuSliceCodec:
         for t in (block, pp, gp, lay.d_ptrs, lay.d_len):
             t.record_stream(side)
         side.wait_stream(cur)   # the tensors' producers and the descriptor uploads
-        _lib.check(_lib.lib().ec_encode_batched_copy(
-            _lib.u8ptr(lay.coeff), k, m, lay.d_ptrs.data_ptr(), lay.d_len.data_ptr(),
-            pp.data_ptr(), gp.data_ptr(), S, U, stream_handle(side, dev)),
-            "ec_encode_batched_copy")
+        _lib_call("ec_encode_batched_copy", lay.coeff, k, m, lay.d_ptrs.data_ptr(),
+                  lay.d_len.data_ptr(), pp.data_ptr(), gp.data_ptr(), S, U, side, dev)
+        return self._stage_block(lay, tensors, block, side, cur, hold)
+
+    def _stage_block(self, lay, tensors, block: torch.Tensor, side, cur,
+                     hold: bool) -> "PendingSlices":
+        """The end of a snapshot once its kernels are enqueued on ``side``:
+        the ``coded`` event (torch's stream waits for it with ``hold``), and a
+        background thread staging the block to host memory.  With
+        ``keep_block`` the block is kept for the next save."""
+        from . import _lib
+        from .codec import stream_handle
+        k, m, U = self.k, self.m, self.unit_bytes
+        S, dev = lay.n_stripes, lay.device
         coded = torch.cuda.Event()
         coded.record(side)
         if hold:
@@ -461,10 +518,68 @@ class GpuSliceCodec:
                     _lib.ptr_array([out[p].ctypes.data for p in range(k + m)]),
                     pinned.data_ptr(), pinned.numel(), self.stage_threads,
                     stream_handle(xfer, dev)), "ec_stage_stripes_to_host")
-            block = None   # back to the allocator: the last transfer has landed
+            self.last_stage_stats = _lib.last_stage_stats()
+            block = None   # back to the allocator (unless kept): the last transfer has landed
             return meta, [out[p] for p in range(k + m)]
 
-        return PendingSlices(coded, stage)
+        kept = block
+        pending = PendingSlices(coded, stage)
+        if self.keep_block:
+            self._resident = (kept, pending)
+        del kept
+        return pending
+
+    def _snapshot_delta(self, lay, tensors, res, changed_tensors,
+                        hold: bool) -> "PendingSlices":
+        """The incremental save of ``snapshot``: the changed tensors' units
+        folded into the kept block (parity update, then the copy of the new
+        units), on the side stream."""
+        from .codec import side_stream
+        block, prev = res
+        prev.wait()   # its staging has read the block
+        k, m, U = self.k, self.m, self.unit_bytes
+        S, dev = lay.n_stripes, lay.device
+        cur = torch.cuda.current_stream(dev)
+        side = side_stream(dev)
+        ct = np.unique(np.asarray(changed_tensors, np.int64).reshape(-1))
+        if ct.size and (ct[0] < 0 or ct[-1] >= len(tensors)):
+            raise ValueError(f"changed_tensors must index the {len(tensors)} tensors")
+        units = np.flatnonzero(np.isin(lay.unit_tensor, ct))
+        desc = ()
+        if units.size:
+            stripe, pos = units // k, units % k
+            st, inv = np.unique(stripe, return_inverse=True)
+            base, row = np.uint64(block.data_ptr()), np.uint64((k + m) * U)
+            old = base + stripe.astype(np.uint64) * row + pos.astype(np.uint64) * np.uint64(U)
+            nptr = np.zeros((st.size, k), np.uint64)
+            optr = np.zeros((st.size, k), np.uint64)
+            ln = np.zeros((st.size, k), np.uint32)
+            nptr[inv, pos] = lay.host_ptrs[stripe, pos]
+            optr[inv, pos] = old
+            ln[inv, pos] = lay.host_len[stripe, pos]
+            pptr = (base + st.astype(np.uint64)[:, None] * row
+                    + (np.uint64(k) + np.arange(m, dtype=np.uint64))[None, :] * np.uint64(U))
+            full = np.full(units.size, U, np.uint32)
+            with torch.cuda.device(dev):
+                up = self._layout._upload
+                desc = (up(nptr.view(np.int64), dev), up(optr.view(np.int64), dev),
+                        up(ln.view(np.int32), dev), up(pptr.view(np.int64), dev),
+                        up(lay.host_ptrs[stripe, pos].view(np.int64), dev),
+                        up(lay.host_len[stripe, pos].view(np.int32), dev),
+                        up(old.view(np.int64), dev), up(full.view(np.int32), dev))
+        for t in (block,) + desc:
+            t.record_stream(side)
+        side.wait_stream(cur)   # the tensors' producers and the descriptor uploads
+        if units.size:
+            d_n, d_o, d_l, d_p, d_src, d_srclen, d_dst, d_full = desc
+            # parity ^= C (new ^ old), old being the block's copy of each unit
+            _lib_call("ec_parity_update", lay.coeff, k, m, d_n.data_ptr(), d_o.data_ptr(),
+                      d_l.data_ptr(), d_p.data_ptr(), int(st.size), U, side, dev)
+            # then the new units over the old ones, zero-padded (a 1 x 1 decode)
+            _lib_call("ec_decode_batched", np.ones((1, 1), np.uint8), 1, 1, d_src.data_ptr(),
+                      d_srclen.data_ptr(), d_dst.data_ptr(), d_full.data_ptr(),
+                      int(units.size), U, side, dev)
+        return self._stage_block(lay, tensors, block, side, cur, hold)
 
     def decode(self, meta: dict, slices: Dict[int, np.ndarray], device) -> List[torch.Tensor]:
         from . import _lib
@@ -537,6 +652,7 @@ class GpuSliceCodec:
                     _lib.ptr_array([a.ctypes.data + c0 * U for a in src]), k, c * U,
                     bufs[b].data_ptr(), C * U, pinned.data_ptr(), pinned.numel(),
                     self.stage_threads, stream_handle(copy, device)), "ec_stage_to_device")
+                self.last_stage_stats = _lib.last_stage_stats()
                 comp.wait_stream(copy)
                 if have:  # the data slices we have go into the tensors
                     h = len(have)
@@ -784,6 +900,12 @@ def _hollow_state(state) -> bytes:
 
 # --------------------------------------------------------------- manager --
 
+def _delta_kw(changed_tensors) -> dict:
+    """The codec keyword of an incremental save (none for a full save, so
+    that codecs without incremental support are called as before)."""
+    return {} if changed_tensors is None else {"changed_tensors": changed_tensors}
+
+
 class ECLocalCheckpointManager:
     """Local (non-persistent) checkpoint manager with erasure-coded
     redundancy, called like the reference's LocalCheckpointManager:
@@ -840,11 +962,22 @@ class ECLocalCheckpointManager:
         return [e[: int(c[0])].numpy() for e, c in zip(every, counts)]
 
     # save
-    def save(self, state, iteration: int, is_async: bool = False):
+    def save(self, state, iteration: int, is_async: bool = False,
+             changed_tensors: Optional[Sequence[int]] = None):
         """Encode this rank's tensors, place the k + m slices on their holders
         and write them.  Collective over the strategy's group.  Raises
         CheckpointingException on every rank if any rank fails; then no slice
         of this iteration is left behind.
+
+        ``changed_tensors`` (not in the reference's call,
+        checkpointing.py:538-541, which saves the whole state every time):
+        the indices, into the state's tensor list, of every tensor whose bytes
+        may have changed since this manager's last save, for a caller that
+        knows (frozen layers, sparse updates).  A codec that keeps its last
+        coded block in HBM (``GpuSliceCodec(keep_block=True)``) then codes
+        only those tensors' units, through the incremental parity update;
+        the slices and files are those of a full save.  Other codecs ignore
+        it.
 
         With is_async the GPU work and the exchange still run here (no GPU
         work may move to a writer process, megatron/core/dist_checkpointing/
@@ -866,14 +999,14 @@ class ECLocalCheckpointManager:
         st = self.strategy
         st.check_group()
         if is_async and self.stage_in_background:
-            return self._save_in_background(state, iteration)
+            return self._save_in_background(state, iteration, changed_tensors)
         self._quiesce()
         error, blobs, slices = None, None, None
         try:
             # .tensors of MCoreTensorAwareStateDict is an iterator: take it once
             tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
             hollow, common = _hollow_state(state), _common(state)
-            meta, slices = st.codec.encode(tensors)
+            meta, slices = st.codec.encode(tensors, **_delta_kw(changed_tensors))
             blobs = self._blobs(meta, slices, hollow, common, iteration)
         except Exception as e:  # noqa: BLE001 - reported collectively below
             error = e
@@ -970,13 +1103,14 @@ class ECLocalCheckpointManager:
         if last is not None:
             last.join()
 
-    def _save_in_background(self, state, iteration: int) -> "AsyncSaveRequest":
+    def _save_in_background(self, state, iteration: int,
+                            changed_tensors: Optional[Sequence[int]] = None) -> "AsyncSaveRequest":
         st = self.strategy
         error, pending, hollow, common = None, None, b"", {}
         try:
             tensors = list(state.tensors) if hasattr(state, "tensors") else list(state)
             hollow, common = _hollow_state(state), _common(state)
-            pending = st.codec.snapshot(tensors)
+            pending = st.codec.snapshot(tensors, **_delta_kw(changed_tensors))
         except Exception as e:  # noqa: BLE001 - reported collectively by the thread
             error = e
         group = self._background_group()

@@ -63,15 +63,30 @@ _side_lock = threading.Lock()
 
 
 def _finish_side_streams() -> None:
-    """At interpreter exit: let the work on the streams of ``side_stream``
-    finish.  The streams themselves are never destroyed here: tensors that
-    outlive this hook (module globals, freed after it) may carry
-    ``record_stream`` uses of them, and the caching allocator records an
-    event on each such stream when it frees them; the end of the process
-    releases the streams with the rest of the HIP context."""
+    """At interpreter exit, before any library's static destructors: let the
+    work on the streams of ``side_stream`` finish, then every device the
+    engine made such a stream on, so that no kernel or copy the engine
+    enqueued is in flight while the process tears down.  (The staging
+    threads of the checkpoint codec are joined before this: their hook is
+    registered after this one, at that module's import, and exit hooks run
+    last-registered first.)  The streams themselves are never destroyed
+    here: tensors that outlive this hook (module globals, freed after it)
+    may carry ``record_stream`` uses of them, and the caching allocator
+    records an event on each such stream when it frees them; the end of the
+    process releases the streams with the rest of the HIP context, as it
+    does torch's own streams."""
     with _side_lock:
+        devices = sorted({idx for idx, _ in _side})
         for s in _side.values():
             s.synchronize()
+    for idx in devices:
+        try:
+            torch.cuda.synchronize(idx)
+        except RuntimeError:   # a device already in error: nothing more to wait for
+            pass
+
+
+atexit.register(_finish_side_streams)
 
 
 def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
@@ -98,8 +113,6 @@ def side_stream(device=None, cus: int = 0) -> torch.cuda.ExternalStream:
             h = ctypes.c_void_p()
             status = _lib.lib().ec_stream_create(idx, key[1], ctypes.byref(h))
             if status == _lib.EC_OK:
-                if not _side:
-                    atexit.register(_finish_side_streams)
                 s = torch.cuda.ExternalStream(h.value, device=torch.device("cuda", idx))
             else:  # the kernels still run; only the overlap with training is lost
                 warnings.warn(f"ec_stream_create on device {idx}: {_lib.strerror(status)}; "

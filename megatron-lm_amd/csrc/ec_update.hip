@@ -1,7 +1,8 @@
-// ec_update.hip — ec_parity_update (update_kernel, k <= 16, m <= 4) and the
-// batched kernels for wide codes (batched_wide_kernel, update_wide_kernel:
-// k at run time, up to EC_MAX_K x EC_MAX_M), which ec_batched.hip and
-// ec_batched_copy.hip reach through batched_wide().
+// ec_update.hip — ec_parity_update (update_kernel of ec_update.h for
+// k <= 16, m <= 4) and the batched kernels for wide codes
+// (batched_wide_kernel, update_wide_kernel: k at run time, up to
+// EC_MAX_K x EC_MAX_M), which ec_batched.hip and ec_batched_copy.hip reach
+// through batched_wide().
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -9,124 +10,10 @@
 #include <utility>
 
 #include "ec_device.h"
+#include "ec_update.h"
 
 namespace ec {
 namespace {
-
-template <int K, int M>
-struct UpdateArgs {
-  const uint64_t* nptr;  // [n_stripes][K], 0 = unit unchanged
-  const uint64_t* optr;  // [n_stripes][K]
-  const uint32_t* len;   // [n_stripes][K]
-  const uint64_t* pptr;  // [n_stripes][M]
-  PermTab tab[M][K];
-  uint32_t unit_bytes;
-  uint32_t tiles_per_unit;   // tiles of B*16 bytes in a unit (B lanes)
-  uint32_t tiles_per_block;  // consecutive tiles one workgroup walks
-  uint32_t blocks_per_unit;
-  FastDiv by_blocks;  // division by blocks_per_unit
-};
-
-// Incremental update: each workgroup walks a span of tiles of one changed
-// stripe.  The stripe's descriptors (which units changed, where their old
-// and new bytes are, their lengths) are read once per span into scalar
-// registers; a tile inside every changed unit, with everything 16-byte
-// aligned, takes plain vector loads, any other tile the byte-granular path.
-template <int K, int M, int B>
-__global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
-  const uint32_t s = fast_div(blockIdx.x, a.by_blocks);
-  const uint32_t t0 = (blockIdx.x - s * a.blocks_per_unit) * a.tiles_per_block;
-  const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
-  // The stripe's descriptors, every entry read unconditionally (the arrays
-  // are dense) so that the reads merge into wide scalar loads in flight
-  // together rather than one dependent round trip per unit.
-  uint64_t np[K], op[K];
-  uint32_t nl[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) np[j] = a.nptr[(uint64_t)s * K + j];
-#pragma unroll
-  for (int j = 0; j < K; ++j) op[j] = a.optr[(uint64_t)s * K + j];
-#pragma unroll
-  for (int j = 0; j < K; ++j) nl[j] = a.len[(uint64_t)s * K + j];
-  __shared__ PermTab tab[M][K];
-  stage_tables<K, M>(tab, a.tab);
-  const uint8_t* nw[K];
-  const uint8_t* od[K];
-  uint32_t len[K];
-  uint32_t full = a.unit_bytes;
-  bool aligned = true, in_aligned = true;
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    nw[j] = reinterpret_cast<const uint8_t*>(np[j]);
-    od[j] = np[j] ? reinterpret_cast<const uint8_t*>(op[j]) : nullptr;
-    const uint32_t l = np[j] ? nl[j] : 0u;
-    len[j] = l < a.unit_bytes ? l : a.unit_bytes;
-    if (nw[j]) {
-      full = len[j] < full ? len[j] : full;
-      in_aligned &=
-          ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
-    }
-  }
-  // Misaligned units (views at arbitrary offsets) are realigned on the fast
-  // path (load_realign); only the parity must be 16-byte aligned for it.  The
-  // aligned case keeps plain loads: realigning every load cost the 1 %
-  // update 5 % (0.338 -> 0.356 ms).
-  uint8_t* p[M];
-#pragma unroll
-  for (int i = 0; i < M; ++i) {
-    p[i] = reinterpret_cast<uint8_t*>(a.pptr[(uint64_t)s * M + i]);
-    aligned &= (reinterpret_cast<uintptr_t>(p[i]) & 15u) == 0;
-  }
-  for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t off = (t * B + threadIdx.x) * 16u;
-    if (off >= a.unit_bytes) continue;
-    const bool fast = aligned && (t + 1) * (B * 16u) <= full;
-    uint32_t acc[M][4] = {};
-    // The parity loads do not depend on the delta: issue them first so that
-    // they are in flight together with the unit loads.
-    uint4 pv[M];
-    if (fast) {
-#pragma unroll
-      for (int i = 0; i < M; ++i) pv[i] = load_stream(p[i] + off);
-    }
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      if (nw[j] == nullptr) continue;  // uniform: unchanged unit
-      if (!fast && off >= len[j]) continue;
-      uint4 vn, vo;
-      if (fast && in_aligned) {
-        vn = load_stream(nw[j] + off);
-        vo = load_stream(od[j] + off);
-      } else if (fast) {
-        vn = load_realign(nw[j], off);
-        vo = load_realign(od[j], off);
-      } else {
-        vn = load_unit(nw[j], off, len[j]);
-        vo = load_unit(od[j], off, len[j]);
-      }
-      const uint4 dl = make_uint4(vn.x ^ vo.x, vn.y ^ vo.y, vn.z ^ vo.z, vn.w ^ vo.w);
-      Fields f[4];
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd) f[dd] = fields(word(dl, dd));
-#pragma unroll
-      for (int i = 0; i < M; ++i) {
-        asm volatile("" ::: "memory");
-        const PermTab tj = tab[i][j];
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) acc[i][dd] = mac1(acc[i][dd], tj, f[dd]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-      const uint4 v = fast ? pv[i] : load_unit(p[i], off, a.unit_bytes);
-      const uint4 w = make_uint4(v.x ^ acc[i][0], v.y ^ acc[i][1], v.z ^ acc[i][2], v.w ^ acc[i][3]);
-      if (fast)
-        store_stream(p[i] + off, w);
-      else
-        store_unit(p[i], off, w);
-    }
-  }
-}
 
 // --------------------------------------- batched kernels for wide codes --
 // The batched encode/decode and the parity update for codes past the
@@ -297,37 +184,28 @@ __global__ void __launch_bounds__(B) update_wide_kernel(const BatchWideArgs a) {
   }
 }
 
-template <int K, int M, int B = kBlock>
-int launch_update(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* optr,
-                  const uint32_t* len, const uint64_t* pptr, uint32_t n_stripes,
-                  uint32_t unit_bytes, hipStream_t st) {
-  UpdateArgs<K, M> a;
-  a.nptr = nptr;
-  a.optr = optr;
-  a.len = len;
-  a.pptr = pptr;
-  for (int i = 0; i < M; ++i)
-    for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
-  const uint32_t unit16 = unit_bytes / 16u;
-  a.unit_bytes = unit_bytes;
-  a.tiles_per_unit = (unit16 + B - 1) / B;
-  // One tile per workgroup: each tile is a dependent chain (unit and parity
-  // loads, then the parity store), so the update wants as many workgroups
-  // in flight as it has tiles.  Measured for the 1 % update of 3,000 ragged
-  // tensors in 64 KiB units (RS(12,4), 2,993 stripes): 3-tile spans 0.382 ms,
-  // one tile 0.343 ms, one tile with the parity loads issued first 0.338 ms.
-  // Spans grow only to keep the grid near 2^30 workgroups.
-  const uint64_t total_tiles = (uint64_t)n_stripes * a.tiles_per_unit;
-  uint64_t tpb = (total_tiles + 0x3fffffffull) >> 30;
-  if (tpb < 1) tpb = 1;
-  if (tpb > a.tiles_per_unit) tpb = a.tiles_per_unit;
-  a.tiles_per_block = (uint32_t)tpb;
-  a.blocks_per_unit = (a.tiles_per_unit + a.tiles_per_block - 1) / a.tiles_per_block;
-  a.by_blocks = make_fastdiv(a.blocks_per_unit);
-  const uint64_t blocks = (uint64_t)n_stripes * a.blocks_per_unit;
-  if (blocks > 0x7fffffffull) return EC_ERANGE;
-  hipLaunchKernelGGL((update_kernel<K, M, B>), dim3((unsigned)blocks), dim3(B), 0, st, a);
-  return hip_status();
+// The update's launch shape (update_kernel in ec_update.h): lanes per
+// workgroup, 16-byte chunks per lane, and log2 of the interleaved slices of
+// the grid (0: launch order).  Measured on MI355X for config 5's 1 % update
+// (RS(12,4), 3,152 changed 64 KiB units in 2,993 stripes, 1.98 GB of
+// traffic), microseconds per launch by lanes x chunks and slices 1 / 8:
+//   256 x 1  322.8 / 311.3     256 x 2  331.6 / 322.0     256 x 4  328.4 / 324.5
+//   128 x 1  331.5 / 309.7     128 x 2  331.0 / 319.6
+//    64 x 1  311.3 / 308.6      64 x 2  365.4 / 320.2      64 x 4  334.1 / 324.5
+// and 64 x 1 over 4 / 16 / 32 slices 307.2 / 314.0 / 315.8: one wavefront on
+// a 1 KiB tile in 4 slices, 0.806 of the HBM roofline against 0.767 for the
+// former 256 x 1 in launch order.  More chunks per lane (more loads in
+// flight per lane, fewer workgroups) lost everywhere.
+constexpr int kUpdateBlock = 64;
+constexpr int kUpdateChunks = 1;
+constexpr uint32_t kUpdateSliceShift = 2;
+
+template <int K, int M>
+int update_fast(const uint8_t* coeff, const uint64_t* nptr, const uint64_t* optr,
+                const uint32_t* len, const uint64_t* pptr, uint32_t n_stripes,
+                uint32_t unit_bytes, hipStream_t st) {
+  return launch_update<K, M, kUpdateBlock, kUpdateChunks>(coeff, nptr, optr, len, pptr, n_stripes,
+                                                          unit_bytes, kUpdateSliceShift, st);
 }
 
 // Wide codes through the batched kernels: encode / decode (update = false,
@@ -399,7 +277,7 @@ using UpdFn = int (*)(const uint8_t*, const uint64_t*, const uint64_t*, const ui
 
 template <int K, int... Ms>
 constexpr auto upd_row(std::integer_sequence<int, Ms...>) {
-  return std::array<UpdFn, sizeof...(Ms)>{&launch_update<K, Ms + 1>...};
+  return std::array<UpdFn, sizeof...(Ms)>{&update_fast<K, Ms + 1>...};
 }
 template <int... Ks>
 constexpr auto upd_table(std::integer_sequence<int, Ks...>) {

@@ -18,21 +18,40 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <chrono>
 
 #include "ec_mi355.h"
 #include "host_copy.h"
 
 namespace {
 
+using Clock = std::chrono::steady_clock;
+
+double seconds_since(Clock::time_point t0) {
+  return std::chrono::duration<double>(Clock::now() - t0).count();
+}
+
+// The timings of this thread's last staging call (ec_stage_last_stats).
+thread_local ec_stage_stats g_last_stats = {};
+
 // The stream's device made current for the call (the events belong on it,
 // whichever device the calling thread has current) and the two events that
 // mark the pinned halves; undone on every return.
+//
+// It also keeps the call's timings: host time blocked in the waits and in
+// the threads' copies, and the device time from the first transfer's start
+// to the last one's end (two timing events), stored for
+// ec_stage_last_stats when the call ends.
 struct Session {
   hipStream_t st;
   int prev = 0;
   bool switched = false;
   hipEvent_t ev[2] = {nullptr, nullptr};
+  hipEvent_t span[2] = {nullptr, nullptr};  // timing events around the transfers
+  bool span_started = false, span_ended = false;
   int status = EC_OK;
+  Clock::time_point start = Clock::now();
+  ec_stage_stats stats = {};
 
   explicit Session(ec_stream_t stream) : st(reinterpret_cast<hipStream_t>(stream)) {
     hipDevice_t sdev = 0;
@@ -49,21 +68,56 @@ struct Session {
     for (auto& e : ev)
       if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess)
         status = EC_EHIP;
+    for (auto& e : span)
+      if (hipEventCreateWithFlags(&e, hipEventBlockingSync) != hipSuccess) status = EC_EHIP;
   }
   ~Session() {
+    if (span_ended) {
+      float ms = 0.0f;
+      if (hipEventSynchronize(span[1]) == hipSuccess &&
+          hipEventElapsedTime(&ms, span[0], span[1]) == hipSuccess)
+        stats.device_s = ms * 1e-3;
+    }
+    stats.wall_s = seconds_since(start);
+    g_last_stats = stats;
     for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
+    for (auto& e : span)
       if (e) (void)hipEventDestroy(e);
     if (switched) (void)hipSetDevice(prev);
   }
   bool ok() const { return status == EC_OK; }
   void fail() { status = EC_EHIP; }
-  // Marks pinned half h as filled by what is enqueued so far.
+  // Before the first transfer: the start of the device-time span.
+  void begin() {
+    if (ok() && !span_started) {
+      if (hipEventRecord(span[0], st) != hipSuccess) fail();
+      span_started = true;
+    }
+  }
+  // Marks pinned half h as filled by what is enqueued so far (one chunk).
   void mark(int h) {
     if (ok() && hipEventRecord(ev[h], st) != hipSuccess) fail();
+    ++stats.chunks;
+  }
+  // After the last transfer: the end of the device-time span.
+  void end() {
+    if (ok() && span_started && hipEventRecord(span[1], st) == hipSuccess) span_ended = true;
   }
   // Waits until the transfers marked on half h have landed.
   void wait(int h) {
+    const Clock::time_point t0 = Clock::now();
     if (ok() && hipEventSynchronize(ev[h]) != hipSuccess) fail();
+    const double w = seconds_since(t0);
+    stats.wait_s += w;
+    stats.max_wait_s = std::max(stats.max_wait_s, w);
+  }
+  // Runs the threads' copy fn(), timed.
+  template <class F>
+  void host_copy(const F& fn) {
+    const Clock::time_point t0 = Clock::now();
+    fn();
+    stats.host_copy_s += seconds_since(t0);
   }
 };
 
@@ -94,6 +148,7 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
   // Chunk j: columns [j * width, min(row_bytes, (j + 1) * width)) of every
   // row, through pinned half j % 2.  The transfer of chunk j is in flight
   // while the threads copy chunk j - 1 out of the other half.
+  ss.begin();
   for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
     if (j < n_chunks) {
       const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
@@ -103,12 +158,15 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                            hipMemcpyDeviceToHost, ss.st) != hipSuccess)
           ss.fail();
       ss.mark(j % 2);
+      if (j + 1 == n_chunks) ss.end();
     }
     if (j >= 1) {
       const uint64_t p = j - 1, x0 = p * width, w = std::min(width, row_bytes - x0);
       ss.wait(p % 2);
       if (!ss.ok()) break;
-      ec::copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
+      ss.host_copy([&] {
+        ec::copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
+      });
     }
   }
   if (!ss.ok()) (void)hipStreamSynchronize(ss.st);  // no transfer outlives the call
@@ -133,6 +191,7 @@ int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_
   // Chunk j: bytes [j * width, ...) of the block, contiguous on the device,
   // in one transfer to pinned half j % 2; the threads scatter chunk j - 1's
   // units into their rows meanwhile.
+  ss.begin();
   for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
     if (j < n_chunks) {
       const uint64_t x0 = j * width, w = std::min(width, total - x0);
@@ -140,12 +199,16 @@ int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_
                          ss.st) != hipSuccess)
         ss.fail();
       ss.mark(j % 2);
+      if (j + 1 == n_chunks) ss.end();
     }
     if (j >= 1) {
       const uint64_t p = j - 1, x0 = p * width, w = std::min(width, total - x0);
       ss.wait(p % 2);
       if (!ss.ok()) break;
-      ec::scatter_units(h_rows, positions, unit_bytes, x0, h_pinned + (p % 2) * half, w, threads);
+      ss.host_copy([&] {
+        ec::scatter_units(h_rows, positions, unit_bytes, x0, h_pinned + (p % 2) * half, w,
+                          threads);
+      });
     }
   }
   if (!ss.ok()) (void)hipStreamSynchronize(ss.st);  // no transfer outlives the call
@@ -175,16 +238,28 @@ int ec_stage_to_device(const uint8_t* const* h_rows, uint32_t rows, uint64_t row
     if (j >= 2) ss.wait(j % 2);
     if (!ss.ok()) break;
     // rows x w bytes, split over the threads by equal shares of bytes
-    ec::gather_rows(pin, h_rows, x0, rows, w, threads);
+    ss.host_copy([&] { ec::gather_rows(pin, h_rows, x0, rows, w, threads); });
+    ss.begin();
     for (uint32_t r = 0; r < rows && ss.ok(); ++r)
       if (hipMemcpyAsync(d_dst + (uint64_t)r * dst_pitch + x0, pin + (uint64_t)r * w, w,
                          hipMemcpyHostToDevice, ss.st) != hipSuccess)
         ss.fail();
     ss.mark(j % 2);
+    if (j + 1 == n_chunks) ss.end();
   }
   // no transfer outlives the call: the pinned buffer is the caller's again
-  if (hipStreamSynchronize(ss.st) != hipSuccess && ss.ok()) ss.fail();
+  {
+    const Clock::time_point t0 = Clock::now();
+    if (hipStreamSynchronize(ss.st) != hipSuccess && ss.ok()) ss.fail();
+    ss.stats.wait_s += seconds_since(t0);
+  }
   return ss.status;
+}
+
+int ec_stage_last_stats(ec_stage_stats* out) {
+  if (!out) return EC_EINVAL;
+  *out = g_last_stats;
+  return EC_OK;
 }
 
 }  // extern "C"

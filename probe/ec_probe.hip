@@ -1,8 +1,6 @@
-// ec_probe.hip — probes that bench.py uses to measure the practical HBM
-// ceiling of the RS kernels' access pattern on the box it runs on, and the
-// alternative GF(2^8) multiply the product's v_perm tables are measured
-// against.  Not part of the C ABI of ec_mi355.h and not used by the product
-// path.
+// ec_probe.hip — the probe bench.py uses to measure the practical HBM
+// ceiling of the RS kernels' access pattern on the box it runs on.  Not part
+// of the C ABI of ec_mi355.h and not used by the product path.
 //
 // probe_kernel<R, W> is the memory skeleton of RS(6,3)'s rs_kernel: one-wave
 // (64-lane) workgroups in launch order, one 16-byte non-temporal load per
@@ -62,109 +60,9 @@ int launch(const ProbeArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-// ---- RS encode with LDS log/exp tables --------------------------------
-//
-// The textbook GF(2^8) multiply: c * x = exp[log c + log x] (x != 0), with
-// log (256 B) and exp (512 B, doubled so the sum needs no reduction) in LDS.
-// Per data byte: one log lookup shared by the m outputs and one exp lookup
-// per output, all byte-granular LDS reads at data-dependent addresses.  Same
-// workgroups, grid and non-temporal 16-byte loads and stores as rs_kernel.
-struct LogExpArgs {
-  const uint8_t* src[kMaxStreams];
-  uint8_t* dst[kMaxStreams];
-  uint8_t log_tab[256];
-  uint8_t exp_tab[512];
-  uint8_t log_coef[kMaxStreams * kMaxStreams];  // [i][j], coefficients non-zero
-  uint64_t n16;
-};
-
-template <int K, int M>
-__global__ void __launch_bounds__(kBlock) logexp_kernel(const LogExpArgs a) {
-  __shared__ uint8_t lg[256];
-  __shared__ uint8_t ex[512];
-  __shared__ uint32_t lc[M][K];
-  for (int t = threadIdx.x; t < 256; t += kBlock) lg[t] = a.log_tab[t];
-  for (int t = threadIdx.x; t < 512; t += kBlock) ex[t] = a.exp_tab[t];
-  if (threadIdx.x < M * K)
-    lc[threadIdx.x / K][threadIdx.x % K] = a.log_coef[(threadIdx.x / K) * kMaxStreams +
-                                                     threadIdx.x % K];
-  __syncthreads();
-  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)blockIdx.x * kBlock + threadIdx.x; idx < a.n16; idx += stride) {
-    u32x4 acc[M];
-#pragma unroll
-    for (int i = 0; i < M; ++i) acc[i] = u32x4{0u, 0u, 0u, 0u};
-    // one data stream at a time keeps the lookups' registers (and so the
-    // occupancy) in line with rs_kernel's
-#pragma unroll 1
-    for (int j = 0; j < K; ++j) {
-      const u32x4 x = load_nt(a.src[j] + idx * 16);
-      uint32_t c[M];
-#pragma unroll
-      for (int i = 0; i < M; ++i) c[i] = lc[i][j];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t v = (x[d] >> (8 * b)) & 0xffu;
-          const uint32_t l = lg[v];
-#pragma unroll
-          for (int i = 0; i < M; ++i) {
-            const uint32_t prod = v ? ex[l + c[i]] : 0u;
-            acc[i][d] ^= prod << (8 * b);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < M; ++i) store_nt(a.dst[i] + idx * 16, acc[i]);
-  }
-}
-
 }  // namespace
 
 extern "C" {
-
-// RS encode over GF(2^8)/0x11D with LDS log/exp tables: out[i] = XOR_j
-// coeff[i*k+j] * src[j], for (k, m) = (6, 3) only, non-zero coefficients,
-// nbytes a multiple of 16 and 16-byte aligned pointers.  Returns 0, -1 (bad
-// arguments) or -4 (launch error).  For comparison with ec_rs_encode only.
-int ecp_rs_logexp(const uint8_t* coeff, int k, int m, const uint8_t* const* src,
-                  uint8_t* const* dst, uint64_t nbytes, void* stream) {
-  if (k != 6 || m != 3 || !coeff || !src || !dst || nbytes % 16) return -1;
-  LogExpArgs a = {};
-  for (int j = 0; j < k; ++j) {
-    if (!src[j] || (reinterpret_cast<uintptr_t>(src[j]) & 15u)) return -1;
-    a.src[j] = src[j];
-  }
-  for (int i = 0; i < m; ++i) {
-    if (!dst[i] || (reinterpret_cast<uintptr_t>(dst[i]) & 15u)) return -1;
-    a.dst[i] = dst[i];
-  }
-  // exp[e] = 2^e in GF(2^8)/0x11D for e in [0, 510], log its inverse on 1..255
-  uint32_t v = 1;
-  for (int e = 0; e < 255; ++e) {
-    a.exp_tab[e] = a.exp_tab[e + 255] = (uint8_t)v;
-    a.log_tab[v] = (uint8_t)e;
-    v <<= 1;
-    if (v & 0x100u) v ^= 0x11Du;
-  }
-  a.exp_tab[510] = a.exp_tab[0];
-  a.exp_tab[511] = a.exp_tab[1];
-  for (int i = 0; i < m; ++i)
-    for (int j = 0; j < k; ++j) {
-      if (!coeff[i * k + j]) return -1;
-      a.log_coef[i * kMaxStreams + j] = a.log_tab[coeff[i * k + j]];
-    }
-  a.n16 = nbytes / 16;
-  if (a.n16 == 0) return 0;
-  const uint64_t tiles = (a.n16 + kBlock - 1) / kBlock;
-  const unsigned grid = (unsigned)(tiles < (1u << 24) ? tiles : (1u << 24));
-  hipLaunchKernelGGL((logexp_kernel<6, 3>), dim3(grid), dim3(kBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
-  return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
 
 // Streams R inputs and W outputs of nbytes each (a multiple of 16, 16-byte
 // aligned pointers) through the skeleton; out[i] = a fixed pattern XOR the

@@ -165,6 +165,9 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             torch.cuda.set_device(0)
             device = "cuda:0"
             codec = None
+            if scenario == "incremental":
+                from megatron_lm_amd.checkpoint import GpuSliceCodec
+                codec = GpuSliceCodec(k, m, unit, keep_block=True)
         else:
             from ec_cpu_codec import OracleSliceCodec
             codec = OracleSliceCodec(k, m, unit)
@@ -384,6 +387,38 @@ def run(rank, world, port, root, scenario, k, m, unit, use_gpu, errfile, jump=1)
             assert mgr.latest_iteration == 4
             got, name = mgr.load()
             assert name == f"iter_0000004_{rank}_local" and same(got.tensors, bumped)
+        elif scenario == "incremental":
+            # Saves that name the tensors changed since the last save: the
+            # first save is full, then one tensor changes per save, through
+            # the synchronous, the async and the background path, and one
+            # save changes nothing.  Every save loads back as the state of
+            # its call, also after a rank loses its storage.  With the GPU
+            # codec (keep_block) the later saves take the incremental path.
+            delta = []
+            if use_gpu:
+                inner = strat.codec._snapshot_delta
+                strat.codec._snapshot_delta = lambda *a, **kw: delta.append(1) or inner(*a, **kw)
+            ts = state.tensors
+            mgr.save(state, 1)
+            bump(ts[0])
+            mgr.save(state, 2, changed_tensors=[0])
+            got, name = mgr.load()
+            assert name == f"iter_0000002_{rank}_local" and same(got.tensors, ts)
+            bump(ts[-1])
+            mgr.save(state, 3, is_async=True, changed_tensors=[len(ts) - 1]).execute_sync()
+            mgr.stage_in_background = True
+            ts[1].view(-1)[:3] = 7   # part of a tensor
+            mgr.save(state, 4, is_async=True, changed_tensors=[1]).execute_sync()
+            mgr.save(state, 5, changed_tensors=[])
+            if rank == world - 1:
+                lose_storage(mgr)
+            dist.barrier()
+            got, name = mgr.load()
+            assert name == f"iter_0000005_{rank}_local" and same(got.tensors, ts)
+            if use_gpu:
+                assert len(delta) == 4, delta
+            else:
+                assert strat.codec.changed_log == [None, [0], [len(ts) - 1], [1], []]
         elif scenario == "background_fail":
             # One rank fails before (fail) or during (fail_late) the
             # background staging: every rank's finalize raises, nothing of

@@ -38,9 +38,10 @@ class OracleSliceCodec:
     def __init__(self, k, m, unit_bytes, fail=False, fail_late=False):
         self.k, self.m, self.unit_bytes, self.fail = k, m, unit_bytes, fail
         self.fail_late = fail_late
+        self.changed_log = []   # the changed_tensors of each call (None: a full save)
 
-    def snapshot(self, tensors):
-        meta, slices = self.encode(tensors)
+    def snapshot(self, tensors, changed_tensors=None):
+        meta, slices = self.encode(tensors, changed_tensors)
         err = RuntimeError("injected staging failure") if self.fail_late else None
         return _Staged(meta, slices, err)
 
@@ -53,7 +54,10 @@ class OracleSliceCodec:
                 lens.append(min(U, b.size - o))
         return units, lens
 
-    def encode(self, tensors):
+    def encode(self, tensors, changed_tensors=None):
+        """The full encode, also when changed_tensors names the tensors that
+        changed (the slices are the same)."""
+        self.changed_log.append(None if changed_tensors is None else list(changed_tensors))
         if self.fail:
             raise RuntimeError("injected encode failure")
         k, m, U = self.k, self.m, self.unit_bytes

@@ -60,6 +60,17 @@ def test_abi_version_and_strerror(pkg):
     assert L.ec_strerror(-99) == b"unknown status"
 
 
+def test_library_missing_an_export_is_refused(pkg, monkeypatch):
+    """A stale library (one that lacks a symbol the binding declares) is
+    refused when it loads, with ECLibraryMissing, not later with an
+    AttributeError on the first call of the missing entry point."""
+    lib_mod = pkg._lib
+    monkeypatch.setattr(lib_mod, "_lib", None)
+    monkeypatch.setattr(lib_mod, "EXPORTS", lib_mod.EXPORTS + ("ec_not_in_this_library",))
+    with pytest.raises(lib_mod.ECLibraryMissing, match="ec_not_in_this_library"):
+        lib_mod.lib()
+
+
 def test_host_gf_mul_inv_match_oracle(pkg):
     t = pyref.mul_table()
     L = pkg._lib.lib()

@@ -32,7 +32,7 @@ def launch(tmp_path, scenario, world=6, k=4, m=2, unit=1024, use_gpu=False, jump
 
 @pytest.mark.parametrize("scenario", ["recover", "cleanup", "failed_save", "too_many_lost", "async",
                                       "async_write_lost", "tasd", "stray", "background",
-                                      "background_fail"])
+                                      "background_fail", "incremental"])
 def test_ec_checkpoint_scenarios(tmp_path, scenario):
     launch(tmp_path, scenario)
 

@@ -63,6 +63,101 @@ def test_gpu_checkpoint_background_three_ranks(tmp_path):
     launch(tmp_path, "background", world=3, k=2, m=1, unit=4096, use_gpu=True)
 
 
+def test_gpu_checkpoint_incremental_three_ranks(tmp_path):
+    """Saves naming the changed tensors, through the GPU codec's kept block
+    (keep_block): every save after the first takes the incremental path and
+    loads back as the state of its call, also after a rank loses its
+    storage."""
+    launch(tmp_path, "incremental", world=3, k=2, m=1, unit=1024, use_gpu=True)
+
+
+def _oracle_slices(k, m, unit, gpu):
+    return OracleSliceCodec(k, m, unit).encode([t.cpu() for t in gpu])
+
+
+@pytest.mark.parametrize("k,m,unit", [(6, 3, 4096), (12, 4, 1024), (4, 2, 256), (2, 1, 65536)])
+def test_gpu_incremental_saves_equal_full_encodes(pkg, dev, k, m, unit):
+    """A keep_block codec over a sequence of saves, each naming the tensors
+    changed since the one before (none, some, all, part of one tensor), also
+    through snapshot() with the next step's writes racing it: every save's
+    slices equal the oracle codec's full encode of the state of its call, and
+    every save after the first takes the incremental path (the kept block is
+    updated in place, not reallocated)."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    cpu = make_tensors(3) + make_tensors(1) + [torch.arange(3001, dtype=torch.int32)]
+    gpu = [t.to(dev) for t in cpu]
+    codec = GpuSliceCodec(k, m, unit, keep_block=True)
+    calls = []
+    inner = codec._snapshot_delta
+    codec._snapshot_delta = lambda *a, **kw: calls.append(1) or inner(*a, **kw)
+    meta, sl = codec.encode(gpu)
+    assert meta == _oracle_slices(k, m, unit, gpu)[0]
+    block = codec._resident[0].data_ptr()
+    codec.release(sl)
+    rng = np.random.default_rng(k * 100 + unit)
+    plans = [[], [0], list(range(len(gpu))), [2, 4], [len(gpu) - 1]]
+    for n, changed in enumerate(plans):
+        for i in changed:
+            bump(gpu[i])
+        if n == 3:   # part of a tensor only: a few bytes of one unit
+            flat = gpu[2].view(-1).view(torch.uint8)
+            flat[int(rng.integers(0, flat.numel() - 4)):][:4] ^= 0x5A
+        want = _oracle_slices(k, m, unit, gpu)
+        if n % 2:
+            pending = codec.snapshot(gpu, changed_tensors=changed)
+            for t in gpu:                      # the next step, after the call
+                t.view(-1).view(torch.uint8).bitwise_xor_(0x5A)
+            meta, sl = pending.result(timeout=120)
+            for t in gpu:                      # undone exactly, as if it never ran
+                t.view(-1).view(torch.uint8).bitwise_xor_(0x5A)
+            torch.cuda.synchronize()
+        else:
+            meta, sl = codec.encode(gpu, changed_tensors=changed)
+        assert meta == want[0], n
+        for p, (a, b) in enumerate(zip(sl, want[1])):
+            assert np.array_equal(a, b), (n, changed, p)
+        codec.release(sl)
+    assert len(calls) == len(plans)
+    assert codec._resident[0].data_ptr() == block
+
+
+def test_gpu_incremental_save_codes_only_the_named_tensors(pkg, dev):
+    """The incremental path codes only the tensors it is told changed: a
+    tensor changed behind its back keeps its old bytes in the slices (the
+    caller's contract; this is what makes the save incremental), and a save
+    over other tensors, or without changed_tensors, takes the full encode."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    k, m, unit = 4, 2, 1024
+    gpu = [t.to(dev) for t in make_tensors(3)]
+    codec = GpuSliceCodec(k, m, unit, keep_block=True)
+    calls = []
+    inner = codec._snapshot_delta
+    codec._snapshot_delta = lambda *a, **kw: calls.append(1) or inner(*a, **kw)
+    before = _oracle_slices(k, m, unit, gpu)
+    codec.release(codec.encode(gpu)[1])
+    orig1 = gpu[1].clone()
+    bump(gpu[0])
+    bump(gpu[1])
+    _, sl = codec.encode(gpu, changed_tensors=[0])   # gpu[1] changed too, unnamed
+    after = _oracle_slices(k, m, unit, gpu)
+    stale = _oracle_slices(k, m, unit, [gpu[0], orig1] + gpu[2:])
+    assert calls == [1]
+    assert all(np.array_equal(a, b) for a, b in zip(sl, stale[1]))
+    assert not all(np.array_equal(a, b) for a, b in zip(sl, after[1]))
+    assert not all(np.array_equal(a, b) for a, b in zip(sl, before[1]))
+    codec.release(sl)
+    # a full save (no changed_tensors) brings the block up to date
+    _, sl = codec.encode(gpu)
+    assert calls == [1] and all(np.array_equal(a, b) for a, b in zip(sl, after[1]))
+    codec.release(sl)
+    # other tensors (other device bytes): the full encode, whatever is named
+    other = [t.clone() for t in gpu]
+    _, sl = codec.encode(other, changed_tensors=[])
+    assert calls == [1] and all(np.array_equal(a, b) for a, b in zip(sl, after[1]))
+    with pytest.raises(ValueError):
+        codec.encode(other, changed_tensors=[7])
+
+
 def test_gpu_empty_tensor_list(pkg, dev):
     """A rank with nothing to save still takes part: one all-zero stripe."""
     from megatron_lm_amd.checkpoint import GpuSliceCodec

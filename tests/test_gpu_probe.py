@@ -60,24 +60,3 @@ def test_probe_rejects_bad_arguments(probe, dev):
     assert probe.ecp_stream(_ptrs([a[1:]]), 1, _ptrs([a]), 1, 32, sink.data_ptr(), st) == -1
     assert probe.ecp_stream(_ptrs([a, a]), 2, _ptrs([a, a]), 2, 32, sink.data_ptr(), st) == -1  # (2, 2) not built
     assert probe.ecp_stream(_ptrs([a]), 1, _ptrs([a]), 1, 32, None, st) == -1
-
-
-def test_logexp_encoder_matches_oracle(probe, dev):
-    """The LDS log/exp RS(6,3) encoder the v_perm kernel is measured against
-    computes the same code (oracle bytes, zero data bytes included)."""
-    import oracle
-    probe.ecp_rs_logexp.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                    ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
-    n = (1 << 20) + 4096 * 3
-    rng = np.random.default_rng(7)
-    host = [rng.integers(0, 256, n, dtype=np.uint8) for _ in range(6)]
-    host[2][::3] = 0
-    C = oracle.cauchy(6, 3)
-    ins = [torch.from_numpy(h).to(dev) for h in host]
-    outs = [torch.zeros(n, dtype=torch.uint8, device=dev) for _ in range(3)]
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    assert probe.ecp_rs_logexp(C.ctypes.data_as(ctypes.c_void_p), 6, 3, _ptrs(ins), _ptrs(outs),
-                               n, st) == 0
-    torch.cuda.synchronize()
-    for o, w in zip(outs, oracle.rs_encode(C, host)):
-        assert np.array_equal(o.cpu().numpy(), w)
