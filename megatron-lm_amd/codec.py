@@ -276,8 +276,13 @@ class ShardPlan:
                 raise ValueError(f"coefficient matrix has {k} columns, got {len(ptrs)} shards")
         self.inputs = list(shards)
         self.outputs = _outputs(out, m, nbytes, device, "out")
+        # Outputs allocated here come from torch's current stream; launched
+        # on another stream, the caching allocator must not hand their memory
+        # out again before that stream's work has run.
+        self._owned = out is None
         self.device, self.what, self.nbytes = device, what, nbytes
         self._stream = stream_handle(stream, device)
+        self._hold_outputs(stream)
         self._fn = getattr(L, what)
         data = _lib.ptr_array(ptrs)
         if what == "ec_xor_encode":
@@ -288,8 +293,21 @@ class ShardPlan:
                           _lib.ptr_array([t.data_ptr() for t in self.outputs]),
                           ctypes.c_uint64(nbytes))
 
+    def _hold_outputs(self, stream) -> None:
+        """record_stream of the plan's own outputs on ``stream`` when that is
+        not the stream they were allocated on."""
+        if not self._owned or stream is None:
+            return
+        if stream.cuda_stream != torch.cuda.current_stream(self.device).cuda_stream:
+            for t in self.outputs:
+                t.record_stream(stream)
+
     def __call__(self, stream=None) -> List[torch.Tensor]:
-        st = self._stream if stream is None else stream_handle(stream, self.device)
+        if stream is None:
+            st = self._stream
+        else:
+            st = stream_handle(stream, self.device)
+            self._hold_outputs(stream)
         status = self._fn(*self._head, st)
         if status != _lib.EC_OK:
             _lib.check(status, self.what)

@@ -310,14 +310,15 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
 // copying encode) a launch is two kernels over disjoint tiles of every
 // stripe:
 //  - batched_full_kernel, one workgroup per tile in launch order, codes the
-//    tiles of an aligned stripe before its first unit end and after its last
-//    one (tile_split), as far as every output covers them, and returns at
-//    once on the others: nothing but the vector path, and the compiler
-//    spreads its unit loads between the GF arithmetic;
+//    tiles of an aligned stripe that hold no unit end strictly inside them,
+//    as far as every output covers them (vector_end, end_inside), and
+//    returns at once on the others: nothing but the vector path, and the
+//    compiler spreads its unit loads between the GF arithmetic;
 //  - batched_rest_kernel, rest_groups workgroups per stripe, codes the other
-//    tiles through code_tile.  A stripe of whole units (a rank's buffer cut
-//    into units: every stripe but the last) returns after reading its
-//    descriptors.
+//    tiles through code_tile: at most k tiles holding a unit end, and the
+//    tiles some output does not cover.  A stripe of whole units (a rank's
+//    buffer cut into units: every stripe but the last) returns after reading
+//    its descriptors.
 // Measured on MI355X over 20.8 GB of data, fraction of the 8 TB/s roofline
 // at 2 / 4 / 8 MiB units, the single kernel (8 slices) -> the two kernels,
 // each pair from one box:
@@ -342,43 +343,50 @@ constexpr bool split_pays() {
   return K == 8 && M == 2;
 }
 
-// The tiles of an aligned stripe that hold an end strictly inside them lie
-// in [first_end, last_end] (empty: first_end > last_end); from out_end on some
-// output does not cover the tile (output i covers tile t iff olen[i] >=
-// (t + 1) * kTileBytes).  batched_full_kernel codes the tiles before
-// first_end and those between last_end and out_end, where every unit covers
-// the tile or ended before it (read as zeros) and every output covers it;
-// batched_rest_kernel the others, and every tile of a stripe with a
-// misaligned address.
-struct TileSplit {
-  uint32_t first_end, last_end, out_end;
-};
-
-template <int K, int M, bool COPY, uint32_t kTileBytes>
-__device__ __forceinline__ TileSplit tile_split(const Stripe<K, M, COPY>& st, uint32_t tiles) {
-  TileSplit sp{tiles, 0u, tiles};
-  bool any = false;
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    const bool inside = st.len[j] % kTileBytes != 0;
-    const uint32_t t = st.len[j] / kTileBytes;
-    sp.first_end = inside && t < sp.first_end ? t : sp.first_end;
-    sp.last_end = inside && t > sp.last_end ? t : sp.last_end;
-    any |= inside;
-  }
-  if (!any) sp.last_end = 0, sp.first_end = tiles;   // no end inside any tile
+// Which tiles of a stripe the vector kernel codes: an aligned stripe's tiles
+// below out_end (from out_end on some output does not cover the tile: output
+// i covers tile t iff olen[i] >= (t + 1) * kTileBytes) that hold no unit end
+// strictly inside them (every unit covers such a tile or ended before it,
+// and reads as zeros there).  batched_rest_kernel codes the others: the at
+// most K tiles below out_end that hold a unit end, then [out_end, tiles);
+// out_end is 0 for a stripe with a misaligned address, whose tiles all go
+// to the rest kernel.
+template <int K, int M, bool COPY>
+__device__ __forceinline__ uint32_t vector_end(const Stripe<K, M, COPY>& st, uint32_t tiles,
+                                               uint32_t tile_bytes) {
+  uint32_t out_end = tiles;
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    const uint32_t t = st.olen[i] / kTileBytes;
-    sp.out_end = t < sp.out_end ? t : sp.out_end;
+    const uint32_t t = st.olen[i] / tile_bytes;
+    out_end = t < out_end ? t : out_end;
   }
-  if (!(st.in_aligned && st.out_aligned)) sp.out_end = 0;   // nothing for the vector kernel
-  return sp;
+  return st.in_aligned && st.out_aligned ? out_end : 0u;
 }
 
-// Whether batched_full_kernel codes tile t.
-__device__ __forceinline__ bool vector_tile(const TileSplit& sp, uint32_t t) {
-  return t < sp.out_end && (t < sp.first_end || t > sp.last_end);
+// Whether a unit of the stripe ends strictly inside tile t.
+template <int K, int M, bool COPY>
+__device__ __forceinline__ bool end_inside(const Stripe<K, M, COPY>& st, uint32_t t,
+                                           uint32_t tile_bytes) {
+  const uint32_t lo = t * tile_bytes, hi = lo + tile_bytes;
+  bool e = false;
+#pragma unroll
+  for (int j = 0; j < K; ++j) e |= st.len[j] > lo && st.len[j] < hi;
+  return e;
+}
+
+// Unit j's end tile when it ends strictly inside a tile below out_end and no
+// unit before it ends in the same tile (so that each end tile is listed
+// once); else tiles (none).
+template <int K, int M, bool COPY>
+__device__ __forceinline__ uint32_t first_end_tile(const Stripe<K, M, COPY>& st, int j,
+                                                   uint32_t out_end, uint32_t tiles,
+                                                   uint32_t tile_bytes) {
+  const uint32_t t = st.len[j] / tile_bytes;
+  if (st.len[j] % tile_bytes == 0 || t >= out_end) return tiles;
+#pragma unroll
+  for (int q = 0; q < K; ++q)
+    if (q < j && st.len[q] % tile_bytes != 0 && st.len[q] / tile_bytes == t) return tiles;
+  return t;
 }
 
 template <int K, int M, int B>
@@ -396,12 +404,13 @@ __global__ void __launch_bounds__(B) batched_full_kernel(const BatchArgs<K, M> a
   Stripe<K, M, false> st;
   stripe_facts(st, r, a.unit_bytes);
   constexpr uint32_t kTileBytes = B * 16u;
-  const TileSplit sp = tile_split<K, M, false, kTileBytes>(st, a.tiles_per_unit);
+  const bool mine = t < vector_end(st, a.tiles_per_unit, kTileBytes) &&
+                    !end_inside(st, t, kTileBytes);
   // A loop of zero or one tile rather than a return and straight-line code:
   // in this form the compiler interleaves the unit loads with the GF
   // arithmetic (RS(8,2): 122 VGPRs against 142 with the loads hoisted), and
   // RS(8,2) over 4 MiB units runs at 0.82 of the roofline against 0.79.
-  const uint32_t t_end = vector_tile(sp, t) ? t + 1 : t;
+  const uint32_t t_end = mine ? t + 1 : t;
   if (t >= t_end) return;   // the rest kernel's
   for (uint32_t u = t; u < t_end; ++u) {
     const uint32_t lo = u * kTileBytes, hi = lo + kTileBytes;
@@ -429,18 +438,30 @@ __global__ void __launch_bounds__(B) batched_rest_kernel(const BatchArgs<K, M> a
   stripe_facts(st, r, a.unit_bytes);
   constexpr uint32_t kTileBytes = B * 16u;
   const uint32_t tiles = a.tiles_per_unit;
-  const TileSplit sp = tile_split<K, M, false, kTileBytes>(st, tiles);
-  // The tiles batched_full_kernel leaves: [first_end, last_end] below
-  // out_end, then [out_end, tiles), numbered in that order and dealt round
-  // robin to the stripe's workgroups.
-  const uint32_t mid_end = sp.last_end < sp.out_end ? sp.last_end + 1 : sp.out_end;
-  const uint32_t mid = sp.first_end < mid_end ? mid_end - sp.first_end : 0u;
-  const uint32_t total = mid + (tiles - sp.out_end);
+  const uint32_t out_end = vector_end(st, tiles, kTileBytes);
+  // The tiles batched_full_kernel leaves: the distinct end tiles below
+  // out_end (at most K), then [out_end, tiles), numbered in that order and
+  // dealt round robin to the stripe's workgroups.
+  uint32_t ends = 0;
+#pragma unroll
+  for (int j = 0; j < K; ++j) ends += first_end_tile(st, j, out_end, tiles, kTileBytes) < tiles;
+  const uint32_t total = ends + (tiles - out_end);
   if (g >= total) return;
   __shared__ PermTab tab[M][K];
   stage_tables<K, M>(tab, a.tab);
   for (uint32_t n = g; n < total; n += a.rest_groups) {
-    const uint32_t t = n < mid ? sp.first_end + n : sp.out_end + (n - mid);
+    uint32_t t = out_end + (n - ends);
+    if (n < ends) {   // the n-th distinct end tile, in unit order
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const uint32_t e = first_end_tile(st, j, out_end, tiles, kTileBytes);
+        if (e < tiles) {
+          if (c == n) t = e;
+          ++c;
+        }
+      }
+    }
     code_tile<K, M, 1, false, B>(a, s, t, st, tab);
   }
 }

@@ -961,6 +961,41 @@ def test_eager_binding_streams_and_operand_checks(pkg, dev):
         pkg.rs_encode(dd[:5] + [d[5]], 3)
 
 
+def test_shard_plan_outputs_held_for_a_launch_on_another_stream(pkg, dev):
+    """A ShardPlan whose outputs it allocated (on torch's current stream)
+    and that launches on another stream, given to the plan or to the call:
+    dropped right after the launch, while that stream still has the launch
+    queued behind a long wait, its outputs' memory is not handed out again
+    (record_stream), and the launch writes the oracle's bytes."""
+    rng = np.random.default_rng(12)
+    n = 1 << 20
+    d = _host(rng, 6, n)
+    dd = _to_dev(d, dev)
+    C = oracle.cauchy(6, 3)
+    want = oracle.rs_encode(C, d)
+    torch.cuda.synchronize()
+    for how in ("plan", "call"):
+        side = torch.cuda.Stream(dev)
+        plan = pkg.ShardPlan(C, dd, stream=side) if how == "plan" else pkg.ShardPlan(C, dd)
+        ptrs = {t.data_ptr() for t in plan.outputs}
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(50_000_000)   # tens of milliseconds of GPU time on side
+        outs = plan() if how == "plan" else plan(stream=side)
+        side_done = torch.cuda.Event()
+        with torch.cuda.stream(side):   # read the outputs on side, after the launch
+            copies = [t.clone() for t in outs]
+            side_done.record(side)
+        del plan, outs
+        fresh = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(3)]
+        assert not ptrs & {t.data_ptr() for t in fresh}, how
+        for t in fresh:
+            t.fill_(0xEE)
+        side_done.synchronize()
+        for c, w in zip(copies, want):
+            assert np.array_equal(c.cpu().numpy(), w), how
+        del fresh, copies
+
+
 def test_flat_kernels_past_the_grid_cap(pkg, dev):
     """Shards of 16 GiB + 4 KiB + 48 B: more 16-byte chunks than the flat
     kernels' one-pass grid covers (2^24 one-wavefront workgroups), so the
