@@ -159,8 +159,22 @@ def cpu_baseline(shards_np, k: int, m: int, seconds: float, gpu_parity, xor_host
                    f"repo CPU encoder ({oracle.fast_isa()}), the reference ships none"),
         "one_core_GBps": enc["one_core_GBps"],
         "isa": oracle.fast_isa(),
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
         "configs": configs,
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_cores() -> int:

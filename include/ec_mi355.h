@@ -202,7 +202,9 @@ int ec_decode_batched(const uint8_t* rows, int k, int e,
  * must be distinct (each parity unit is read-modified-written by one
  * workgroup).  Same alignment rules and limits as ec_encode_batched.  Serves repeated
  * manager.save calls (checkpointing.py:538-541) when only part of the state
- * changed since the previous checkpoint. */
+ * changed since the previous checkpoint: a save that names its changed
+ * tensors folds them into the coded block the last save left in HBM (old =
+ * that block's copy of each unit, parity = its parity units). */
 int ec_parity_update(const uint8_t* coeff, int k, int m,
                      const uint64_t* d_new_ptrs, const uint64_t* d_old_ptrs,
                      const uint32_t* d_len, const uint64_t* d_parity_ptrs,

@@ -121,6 +121,43 @@ def test_gpu_incremental_saves_equal_full_encodes(pkg, dev, k, m, unit):
     assert codec._resident[0].data_ptr() == block
 
 
+def test_gpu_incremental_saves_over_misaligned_views(pkg, dev):
+    """Tensors that are views of one flat buffer at odd byte offsets (the
+    update and the unit copy take their realigning and byte-granular paths):
+    incremental saves equal the oracle codec's full encodes, with the bytes
+    between the views left alone."""
+    from megatron_lm_amd.checkpoint import GpuSliceCodec
+    k, m, unit = 6, 3, 2048
+    rng = np.random.default_rng(31)
+    sizes = [int(x) for x in rng.integers(1, 5 * unit, 9)]
+    arena = torch.full((sum(sizes) + 7 * len(sizes),), 0xC3, dtype=torch.uint8, device=dev)
+    views, off = [], 0
+    for n in sizes:
+        off += int(rng.integers(1, 7))
+        v = arena[off: off + n]
+        v.copy_(torch.from_numpy(rng.integers(0, 256, n, dtype=np.uint8)))
+        views.append(v)
+        off += n
+    gaps = arena.clone()
+    codec = GpuSliceCodec(k, m, unit, keep_block=True)
+    codec.release(codec.encode(views)[1])
+    for changed in ([3], [0, 8], [], list(range(9)), [5]):
+        for i in changed:
+            views[i].bitwise_xor_(torch.from_numpy(
+                rng.integers(1, 256, sizes[i], dtype=np.uint8)).to(dev))
+        meta, sl = codec.encode(views, changed_tensors=changed)
+        want = _oracle_slices(k, m, unit, views)
+        assert meta == want[0]
+        for p, (a, b) in enumerate(zip(sl, want[1])):
+            assert np.array_equal(a, b), (changed, p)
+        codec.release(sl)
+    covered = torch.zeros_like(arena, dtype=torch.bool)
+    for v in views:
+        start = v.data_ptr() - arena.data_ptr()
+        covered[start: start + v.numel()] = True
+    assert torch.equal(arena[~covered], gaps[~covered])
+
+
 def test_gpu_incremental_save_codes_only_the_named_tensors(pkg, dev):
     """The incremental path codes only the tensors it is told changed: a
     tensor changed behind its back keeps its old bytes in the slices (the
