@@ -164,12 +164,10 @@ class PendingSlices:
     def done(self) -> bool:
         return self._done.is_set()
 
-    def wait(self) -> None:
-        """Wait until the staging has ended (its transfers have landed or it
-        failed), without raising what it raised."""
-        self._done.wait()
-        if self._thread is not None:
-            self._thread.join()
+    def staged_event(self) -> threading.Event:
+        """An event set once the staging has ended (its transfers have landed
+        or it failed); holding it does not keep the slices alive."""
+        return self._done
 
     def result(self, timeout: Optional[float] = None) -> Tuple[dict, List[np.ndarray]]:
         if not self._done.wait(timeout):
@@ -244,9 +242,11 @@ class GpuSliceCodec:
         self._host_lock = threading.Lock()
         self._last_layout = None   # descriptors of the last encode, without its tensors
         self._last_ptrs = None     # (block key, parity table, data table) of the last snapshot
-        # keep_block: (block, PendingSlices staging it) of the last save, when
-        # that save coded the whole state into one block (the snapshot path)
-        self._resident: Optional[Tuple[torch.Tensor, "PendingSlices"]] = None
+        # keep_block: (block, event set when its staging has ended) of the last
+        # save, when that save coded the whole state into one block (the
+        # snapshot path).  Not the PendingSlices itself: that holds the slices,
+        # and the codec keeps no reference to a host array it handed out.
+        self._resident: Optional[Tuple[torch.Tensor, threading.Event]] = None
         # ec_stage_last_stats of the last staging call (a diagnostic: the
         # transfer waits, host copies and device time of that call)
         self.last_stage_stats: Optional[dict] = None
@@ -525,7 +525,7 @@ class GpuSliceCodec:
         kept = block
         pending = PendingSlices(coded, stage)
         if self.keep_block:
-            self._resident = (kept, pending)
+            self._resident = (kept, pending.staged_event())
         del kept
         return pending
 
@@ -535,8 +535,8 @@ class GpuSliceCodec:
         folded into the kept block (parity update, then the copy of the new
         units), on the side stream."""
         from .codec import side_stream
-        block, prev = res
-        prev.wait()   # its staging has read the block
+        block, staged = res
+        staged.wait()   # the last save's staging has read the block
         k, m, U = self.k, self.m, self.unit_bytes
         S, dev = lay.n_stripes, lay.device
         cur = torch.cuda.current_stream(dev)

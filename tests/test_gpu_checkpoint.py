@@ -191,6 +191,13 @@ def test_gpu_incremental_save_codes_only_the_named_tensors(pkg, dev):
     other = [t.clone() for t in gpu]
     _, sl = codec.encode(other, changed_tensors=[])
     assert calls == [1] and all(np.array_equal(a, b) for a, b in zip(sl, after[1]))
+    # the kept block does not keep the slices' host array alive
+    import gc
+    import weakref
+    host = weakref.ref(sl[0].base)
+    del sl
+    gc.collect()
+    assert host() is None
     with pytest.raises(ValueError):
         codec.encode(other, changed_tensors=[7])
 
