@@ -415,7 +415,8 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     # each further run folds the same delta in again (timing only)
     w, e = steady(lambda: lay.run(plan), 10, 2)
     changed_bytes = int(lay.host_len.reshape(-1)[changed].sum())
-    upd_traffic = 2 * changed_bytes + 2 * plan.n_stripes * 4 * U5
+    upd_read, upd_write = update_bytes(lay, changed)
+    upd_traffic = upd_read + upd_write
     out["update_1pct_changed_GB"] = round(changed_bytes / 1e9, 3)
     out["update_1pct_ms"] = round(e, 3)
     out["update_1pct_traffic_GBps"] = round(upd_traffic / (e * 1e-3) / 1e9, 1)
@@ -809,6 +810,21 @@ def small_shards(pkg, dev) -> dict:
     return out
 
 
+def update_bytes(lay, changed):
+    """(read, write) algorithmic bytes of the incremental update of the
+    units ``changed``: the new and old bytes of each changed unit, and the m
+    parity units of each changed stripe up to the stripe's longest changed
+    unit (past it the delta is zero, and the kernel leaves the parity
+    alone), read and written back."""
+    import numpy as np
+    lens = lay.host_len.reshape(-1)[changed].astype(np.int64)
+    stripes, inv = np.unique(np.asarray(changed) // lay.k, return_inverse=True)
+    longest = np.zeros(stripes.size, np.int64)
+    np.maximum.at(longest, inv, lens)
+    parity = lay.m * int(longest.sum())
+    return 2 * int(lens.sum()) + parity, parity
+
+
 def ragged_tensors(synth, dev, seed: int, with_host: bool = False):
     """Config 5's 3,000 tensors (bf16 / fp32, log-uniform 4 KiB - 64 MiB),
     drawn on the host (synth.ragged_host) and uploaded one by one; with
@@ -885,9 +901,7 @@ def batched_pmc_launches(pkg, synth, dev, seed: int) -> int:
     changed = synth.perturbed_units(seed, lay.n_units, 0.01)
     olds = [lay.unit_view(u).clone() for u in changed.tolist()]
     uplan = lay.plan_update(par, changed, olds)
-    cb = int(lay.host_len.reshape(-1)[changed].sum())
-    three("c5_update", lambda: lay.run(uplan), 2 * cb + uplan.n_stripes * m * U,
-          uplan.n_stripes * m * U)
+    three("c5_update", lambda: lay.run(uplan), *update_bytes(lay, changed))
     del lay, par, dplan, uplan, olds, tensors
     torch.cuda.empty_cache()
     host = synth.gpt_rank_buffer_host(seed)

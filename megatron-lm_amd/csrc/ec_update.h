@@ -44,7 +44,9 @@ struct UpdateArgs {
 // U * (M + 2) loads in flight.  Misaligned units (views at arbitrary
 // offsets) are realigned there (load_realign); the aligned case keeps plain
 // loads (realigning every load cost the 1 % update 5 %).  Any other tile
-// takes the byte-granular path one chunk at a time.
+// takes the byte-granular path one chunk at a time.  Parity chunks that
+// start at or past the end of the stripe's longest changed unit are neither
+// read nor written: the delta is zero there.
 template <int K, int M, int B, int U>
 __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
   const uint32_t b = span_of(a.grid);
@@ -66,6 +68,7 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
   const uint8_t* od[K];
   uint32_t len[K];
   uint32_t full = a.unit_bytes;   // shortest changed unit
+  uint32_t longest = 0;           // longest changed unit: past it the delta is zero
   bool aligned = true, in_aligned = true;
 #pragma unroll
   for (int j = 0; j < K; ++j) {
@@ -75,6 +78,7 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
     len[j] = l < a.unit_bytes ? l : a.unit_bytes;
     if (nw[j]) {
       full = len[j] < full ? len[j] : full;
+      longest = len[j] > longest ? len[j] : longest;
       in_aligned &=
           ((reinterpret_cast<uintptr_t>(nw[j]) | reinterpret_cast<uintptr_t>(od[j])) & 15u) == 0;
     }
@@ -88,6 +92,7 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
   constexpr uint32_t kTile = B * U * 16u;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t lo = t * kTile;
+    if (lo >= longest) break;   // uniform: no changed byte from here on
     if (aligned && lo + kTile <= full) {
       uint4 pv[U][M];
 #pragma unroll
@@ -135,11 +140,12 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
                                   pv[u][i].z ^ acc[u][i][2], pv[u][i].w ^ acc[u][i][3]));
       continue;
     }
-    // edge tile: a changed unit ends inside it, or the parity is misaligned
+    // edge tile: a changed unit ends inside it or before it, or the parity
+    // is misaligned; parity bytes past the longest changed unit stay as they are
 #pragma unroll 1
     for (int u = 0; u < U; ++u) {
       const uint32_t off = lo + (u * B + threadIdx.x) * 16u;
-      if (off >= a.unit_bytes) continue;
+      if (off >= longest) continue;
       uint32_t acc[M][4] = {};
 #pragma unroll
       for (int j = 0; j < K; ++j) {

@@ -162,9 +162,11 @@ __global__ void __launch_bounds__(B) update_wide_kernel(const BatchWideArgs a) {
   const uint32_t t1 = min(t0 + a.tiles_per_block, a.tiles_per_unit);
   stage_wide<M, B>(w, a, s, true);
   const int k = a.k;
+  uint32_t longest = 0;   // past the longest changed unit the delta is zero
+  for (int j = 0; j < k; ++j) longest = w.len[j] > longest ? w.len[j] : longest;
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t off = t * kWideTile + threadIdx.x * 16u;
-    if (off >= a.unit_bytes) continue;
+    if (off >= longest) continue;
     uint32_t acc[M][4] = {};
     uint4 pv[M];  // the parity does not depend on the delta: load it first
 #pragma unroll

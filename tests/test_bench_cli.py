@@ -29,3 +29,22 @@ def test_help_lists_the_modes():
         assert mode in r.stdout, mode
     for opt in ("--gpus", "--steps", "--warmup", "--settle-ms"):
         assert opt in r.stdout, opt
+
+
+def test_update_bytes_counts_parity_up_to_the_longest_changed_unit():
+    """The update's algorithmic bytes: new + old of each changed unit, and m
+    parity units per changed stripe read and written up to that stripe's
+    longest changed unit."""
+    import types
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import bench
+    # k = 3, m = 2, 100-byte units; stripe 0 full, stripe 1 with a 40-byte unit
+    lay = types.SimpleNamespace(k=3, m=2, host_len=np.array([[100, 100, 100], [100, 40, 0]],
+                                                             np.uint32))
+    read, write = bench.update_bytes(lay, np.array([0, 2, 4]))
+    # changed: unit 0 (100 B) and 2 (100 B) of stripe 0, unit 4 (40 B) of stripe 1
+    assert write == 2 * 100 + 2 * 40
+    assert read == 2 * (100 + 100 + 40) + write
+    read, write = bench.update_bytes(lay, np.array([3, 4]))
+    assert write == 2 * 100 and read == 2 * 140 + 200
