@@ -9,8 +9,8 @@ incremental parity update.
 Modules:
   codec    equal-size shards: xor_encode, rs_encode, reconstruct, ShardPlan (a
            prepared call for repeated launches), host algebra
-  layout   ragged tensor lists -> units -> stripes; batched encode/decode/update
-  api      the drop-in entry points encode / decode / update
+  layout   ragged tensor lists -> units -> stripes; batched encode/decode/update,
+           and the drop-in entry points encode / decode / update
   checkpoint  ECLocalCheckpointManager + ErasureCodedStrategy (the repl_strategy slot)
   args     --non-persistent-ckpt-type in_memory: flags, validation, checkpointing context
 """
@@ -18,8 +18,7 @@ from . import _lib
 from ._lib import ECError, ECLibraryMissing, SingularError
 from .codec import (ShardPlan, cauchy_matrix, decode_matrix, gf_inv, gf_invert, gf_mul, matvec,
                     reconstruct, rs_encode, side_stream, xor_encode)
-from .layout import StripeLayout
-from .api import ParitySet, decode, encode, update
+from .layout import ParitySet, StripeLayout, decode, encode, update
 
 __all__ = [
     "ECError", "ECLibraryMissing", "SingularError", "ShardPlan", "cauchy_matrix", "decode_matrix",

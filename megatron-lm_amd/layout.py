@@ -359,3 +359,50 @@ class StripeLayout:
         flat = t.view(-1).view(torch.uint8) if t.dim() else t.view(1).view(torch.uint8)
         off = int(self.unit_index[u]) * self.unit_bytes
         return flat[off: off + int(self.host_len.reshape(-1)[u])]
+
+
+# --------------------------------------------- drop-in tensor-list entry points --
+# The reference hands MCoreTensorAwareStateDict's ragged tensor list
+# (tensor_aware_state_dict.py:179-184) to LocalCheckpointManager.save
+# (checkpointing.py:538-541), whose redundancy is full replication; these
+# compute m-of-(k+m) parity over the same list instead, and rebuild lost units
+# from it (manager.load, checkpointing.py:891-894):
+#
+#     pset = encode(tasd_tensors, k=12, m=4, unit_bytes=64 << 10)  # parity on HBM
+#     decode(pset, lost=[0, 13])                 # rebuild those positions in place
+#     update(pset, changed_units, old_copies)    # fold a partial change in
+
+@dataclass
+class ParitySet:
+    """Parity of a ragged tensor list: ``parity[s, i]`` is parity unit i of
+    stripe s (uint8, [n_stripes, m, unit_bytes]) under ``layout``."""
+    layout: StripeLayout
+    parity: torch.Tensor
+
+    @property
+    def k(self) -> int:
+        return self.layout.k
+
+    @property
+    def m(self) -> int:
+        return self.layout.m
+
+
+def encode(tensors: Sequence[torch.Tensor], k: int, m: int, unit_bytes: int = 64 << 10,
+           coeff: Optional[np.ndarray] = None, stream=None) -> ParitySet:
+    """Erasure-code a rank's ordered shard tensors in one batched launch."""
+    layout = StripeLayout(tensors, k, m, unit_bytes, coeff)
+    return ParitySet(layout, layout.encode(stream=stream))
+
+
+def decode(pset: ParitySet, lost: Sequence[int], stripes=None, stream=None) -> None:
+    """Rebuild the units at codeword positions ``lost`` (0..k-1 data, k..k+m-1
+    parity) of every stripe (or of ``stripes``) in place."""
+    pset.layout.decode(pset.parity, lost, stripes=stripes, stream=stream)
+
+
+def update(pset: ParitySet, changed_units: Sequence[int], old_units: Sequence[torch.Tensor],
+           stream=None) -> None:
+    """Incremental parity update after the units ``changed_units`` changed;
+    ``old_units`` hold their previous bytes."""
+    pset.layout.update(pset.parity, changed_units, old_units, stream=stream)
