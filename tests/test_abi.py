@@ -139,6 +139,27 @@ def test_device_entry_points_reject_bad_arguments(pkg):
     assert L.ec_encode_batched_copy(c, 6, 3, one, one, one, one, 0, 64, None) == pkg._lib.EC_OK
     assert L.ec_decode_batched(c, 6, 3, one, one, one, None, 1, 64, None) == pkg._lib.EC_EINVAL
     assert L.ec_parity_update(c, 6, 3, one, one, None, one, 1, 64, None) == pkg._lib.EC_EINVAL
+    assert L.ec_stage_last_stats(None) == pkg._lib.EC_EINVAL
+
+
+def test_stage_stats_struct_matches_the_header(pkg):
+    """The ctypes mirror of ec_stage_stats has the header's fields, in order,
+    with the C layout (a uint32 then five doubles: 48 bytes), and a thread
+    that staged nothing reads zeros."""
+    import ctypes
+    import threading
+    text = open(HEADER).read()
+    end = text.index("} ec_stage_stats;")
+    body = text[text.rindex("typedef struct {", 0, end): end]
+    names = re.findall(r"\b(?:uint32_t|double)\s+(\w+);", body)
+    assert names == [n for n, _ in pkg._lib.StageStats._fields_]
+    assert ctypes.sizeof(pkg._lib.StageStats) == 48
+    got = {}
+    t = threading.Thread(target=lambda: got.update(pkg._lib.last_stage_stats()))
+    t.start()
+    t.join()
+    assert got == {"chunks": 0, "wall_s": 0.0, "wait_s": 0.0, "host_copy_s": 0.0,
+                   "max_wait_s": 0.0, "device_s": 0.0}
 
 
 def test_shard_binding_loads_and_checks_operands(pkg):

@@ -834,10 +834,21 @@ def test_stage_stripes_to_host(pkg, dev, stripes, positions, unit, pinned, threa
     _lib.check(_lib.lib().ec_stage_stripes_to_host(
         block.data_ptr(), stripes, positions, unit, _lib.ptr_array([r.ctypes.data for r in rows]),
         pin.data_ptr(), pinned, threads, None), "ec_stage_stripes_to_host")
+    st = _lib.last_stage_stats()
     want = block.cpu().numpy()
     for p in range(positions):
         assert np.array_equal(rows[p][:stripes * unit], want[:, p, :].reshape(-1)), p
         assert (rows[p][stripes * unit:] == 0x77).all(), p
+    # the call's timings: one transfer per pinned half (whole pages when the
+    # half holds at least one) of the block
+    total = stripes * positions * unit
+    half = pinned // 2
+    half = min(half - half % 4096 if half >= 4096 else half, total)
+    assert st["chunks"] == -(-total // half)
+    assert 0 <= st["device_s"] <= st["wall_s"] and 0 <= st["wait_s"] <= st["wall_s"]
+    if total >= 1 << 20:   # long enough for the timing events to tell apart
+        assert st["device_s"] > 0
+    assert 0 <= st["host_copy_s"] <= st["wall_s"] and st["max_wait_s"] <= st["wait_s"]
 
 
 @pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [
