@@ -56,6 +56,15 @@ struct BatchArgs {
 // B * U <= 1024.)
 __device__ __align__(16) uint8_t g_zero_tile[1024 * 16] = {0};
 
+// Store of 16 bytes at base + rel for tile_full (base wave-uniform).
+template <bool WAVE>
+__device__ __forceinline__ void tile_store(uint8_t* base, uint32_t rel, const uint4& v) {
+  if constexpr (WAVE)
+    store_wave<kPolicyNt | kPolicySc1>(base, rel, v);
+  else
+    store_stream(base + rel, v);
+}
+
 // One tile of a stripe in which no unit ends strictly inside the tile and
 // every output covers it (almost every tile).  src[j] points at the tile's
 // first byte of unit j, or at g_zero_tile if the unit ended before the tile;
@@ -66,7 +75,19 @@ __device__ __align__(16) uint8_t g_zero_tile[1024 * 16] = {0};
 // With COPY, cpy[j] points at the tile's first byte of unit j's copy (null:
 // no copy) and the loaded chunk is stored there too: the data is read once
 // for both the parity and the copy.
-template <int K, int M, int U, bool COPY, int B>
+//
+// WAVE selects the access forms.  The tile's addresses are wave-uniform, so
+// with WAVE the loads are nt buffer loads and the stores nt+sc1 buffer
+// stores on those bases (load_wave / store_wave); without, global nt loads
+// and stores.  batched_kernel takes WAVE; batched_full_kernel and
+// batched_rest_kernel do not.  Measured on MI355X (us per launch, global ->
+// WAVE, same box): config 5 encode 4115 -> 4086, its decode of 4 positions
+// 4413 -> 4341, its copying encode 7654 -> 7465; one 20.8 GB buffer through
+// batched_kernel: RS(8,2) in 64 KiB units 3792 -> 3712, 1 MiB 3936 -> 3886,
+// RS(12,4) 4 MiB 4625 -> 4608, 1 MiB 4415 -> 4372, RS(6,3) 1 MiB 4690 ->
+// 4624, 4 MiB 5068 -> 5005.  batched_full_kernel (config 4) went the other
+// way: 3934 -> 4358 with WAVE, 4029 with global loads and sc1 buffer stores.
+template <int K, int M, int U, bool COPY, int B, bool WAVE>
 __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
                                           uint8_t* const (&cpy)[K],
                                           const PermTab (&tab)[M][K]) {
@@ -76,7 +97,8 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
   for (int u = 0; u < U; ++u) {
     const uint32_t rel = (u * B + threadIdx.x) * 16u;
 #pragma unroll
-    for (int j = 0; j < K; ++j) x[u][j] = load_stream(src[j] + rel);
+    for (int j = 0; j < K; ++j)
+      x[u][j] = WAVE ? load_wave(src[j], rel) : load_stream(src[j] + rel);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -85,11 +107,11 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
     gf_matvec16<K, M>(acc, x[u], tab);
 #pragma unroll
     for (int i = 0; i < M; ++i)
-      store_stream(dst[i] + rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      tile_store<WAVE>(dst[i], rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
     if constexpr (COPY) {
 #pragma unroll
       for (int j = 0; j < K; ++j)
-        if (cpy[j]) store_stream(cpy[j] + rel, x[u][j]);
+        if (cpy[j]) tile_store<WAVE>(cpy[j], rel, x[u][j]);
     }
   }
 }
@@ -253,7 +275,7 @@ __device__ __forceinline__ void stripe_facts(Stripe<K, M, COPY>& st,
 // tile when some unit ends strictly inside it or some output does not cover
 // it (or an output is misaligned); a full tile with every unit aligned takes
 // tile_full, one with misaligned units tile_full_realign.
-template <int K, int M, int U, bool COPY, int B>
+template <int K, int M, int U, bool COPY, int B, bool WAVE>
 __device__ __forceinline__ void code_tile(const BatchArgs<K, M>& a, uint32_t s, uint32_t t,
                                           const Stripe<K, M, COPY>& st,
                                           const PermTab (&tab)[M][K]) {
@@ -279,7 +301,7 @@ __device__ __forceinline__ void code_tile(const BatchArgs<K, M>& a, uint32_t s, 
   if (edge)
     tile_edge<K, M, U, COPY, B>(a, s, base, tab);
   else if (st.in_aligned)
-    tile_full<K, M, U, COPY, B>(src, dst, cpy, tab);
+    tile_full<K, M, U, COPY, B, WAVE>(src, dst, cpy, tab);
   else
     tile_full_realign<K, M, U, COPY, B>(src, dst, cpy, tab);
 }
@@ -302,7 +324,7 @@ __global__ void __launch_bounds__(B) batched_kernel(const BatchArgs<K, M> a) {
   stage_tables<K, M>(tab, a.tab);
   Stripe<K, M, COPY> st;
   stripe_facts(st, r, a.unit_bytes);
-  for (uint32_t t = t0; t < t1; ++t) code_tile<K, M, U, COPY, B>(a, s, t, st, tab);
+  for (uint32_t t = t0; t < t1; ++t) code_tile<K, M, U, COPY, B, true>(a, s, t, st, tab);
 }
 
 // ---- large units: the full tiles and the rest, as two kernels ----------
@@ -424,7 +446,7 @@ __global__ void __launch_bounds__(B) batched_full_kernel(const BatchArgs<K, M> a
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) dst[i] = st.p[i] + lo;
-    tile_full<K, M, 1, false, B>(src, dst, cpy, tab);
+    tile_full<K, M, 1, false, B, false>(src, dst, cpy, tab);
   }
 }
 
@@ -462,7 +484,7 @@ __global__ void __launch_bounds__(B) batched_rest_kernel(const BatchArgs<K, M> a
         }
       }
     }
-    code_tile<K, M, 1, false, B>(a, s, t, st, tab);
+    code_tile<K, M, 1, false, B, false>(a, s, t, st, tab);
   }
 }
 

@@ -129,6 +129,38 @@ __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
   __builtin_nontemporal_store(w, (global_u32x4*)(uintptr_t)p);
 }
 
+// The same accesses as buffer instructions on a wave-uniform base: the
+// resource descriptor sits in SGPRs and each lane adds its byte offset
+// (lane_off < 2^31).  The caller guarantees that base is the same for every
+// lane of the wavefront (a kernel argument or descriptor entry plus a
+// workgroup offset); a divergent base would not compile to one descriptor.
+// Cache-policy bits of the buffer forms: 2 = nt (streaming), 16 = sc1.
+// Measured on MI355X (HIP events, same box, loads and stores of the product
+// kernels swapped one at a time): XOR(4) over 4 x 64 MiB 52.6 us with
+// global nt loads and plain stores, 50.9 with sc1 buffer stores, 48.9 with
+// nt buffer loads as well (4 x 256 MiB: 200.7 / 196.4 / 191.9).  The gain
+// depends on the box: on one of eight it was nil.  Which kernel takes which
+// form is stated at each kernel.
+constexpr int kPolicyNt = 2;
+constexpr int kPolicySc1 = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wave_rsrc(const void* base) {
+  // dword 3 = 0x00020000: 32-bit data format, no swizzle, as gfx9 raw
+  // buffers take it; num_records covers any lane offset below 2^31
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 load_wave(const void* base, uint32_t lane_off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wave_rsrc(base), lane_off, 0, kPolicyNt);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int POLICY>
+__device__ __forceinline__ void store_wave(void* base, uint32_t lane_off, const uint4& v) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, wave_rsrc(base), lane_off, 0, POLICY);
+}
+
 // Copy the m x k permute tables from the kernel arguments into LDS, where
 // the unrolled loops read them as wave-uniform broadcasts straight into
 // VGPRs (v_perm_b32 may read only one SGPR, so tables held in SGPRs cost a

@@ -47,7 +47,44 @@ constexpr int flat_block() {
   return K * M <= 20 ? 64 : 128;
 }
 
+// Three forms of the same kernel, chosen per code by flat_form:
+//  - kFormLanes: a per-lane grid-stride loop over 16-byte chunks, global nt
+//    loads and stores (each lane computes its own 64-bit addresses);
+//  - kFormPass: workgroup b codes the B chunks at chunk b * B of every shard
+//    in one pass, global nt loads and stores on a wave-uniform base (kernel
+//    argument plus b * B * 16, a scalar) plus the lane's 16-byte offset;
+//  - kFormPassSc1: the same with nt+sc1 buffer stores on that base
+//    (store_wave).
+// The pass forms cover shards up to 16 GiB in one grid (grid_of); PASSES
+// adds a wave-uniform grid-stride loop for larger ones (the loop costs
+// 0.5-1 % where it is not needed: RS(6,3) over 6 x 256 MiB 372.9 us
+// loop-free against 376.3 with the loop).
+enum FlatForm : int { kFormLanes = 0, kFormPass = 1, kFormPassSc1 = 2 };
+
+// Every shape with k <= 16, m <= 4 was timed in all three forms over 128 MiB
+// shards on two boxes (HIP events, 3 interleaved rounds each).  A pass form
+// is used where it beat kFormLanes by at least 0.5 % on the mean of both
+// boxes (time relative to kFormLanes):
+//   kFormPassSc1: RS(1,1) 0.981, RS(1,2) 0.972, RS(1,3) 0.988, RS(4,3) 0.991,
+//                 RS(4,4) 0.984, RS(5,3) 0.993, RS(6,3) 0.992
+//   kFormPass:    RS(1,4) 0.982, RS(4,1) 0.988, RS(7,2) 0.982, RS(12,1) 0.993,
+//                 RS(13,1) 0.989, RS(16,1) 0.960
+// kFormLanes was ahead for most codes with k >= 7 (by up to 3-4 %: RS(10,3)
+// 1.022 / 1.041 for the pass forms, RS(9,2) 1.025 / 1.029), and the rest lie
+// within 0.5 %.  The headline shape, RS(6,3) over 6 x 256 MiB, in the same
+// library on one box: 375.9 us (kFormLanes) against 371.2 (kFormPassSc1).
 template <int K, int M>
+constexpr int flat_form() {
+  constexpr int kSc1[][2] = {{1, 1}, {1, 2}, {1, 3}, {4, 3}, {4, 4}, {5, 3}, {6, 3}};
+  constexpr int kPass[][2] = {{1, 4}, {4, 1}, {7, 2}, {12, 1}, {13, 1}, {16, 1}};
+  for (const auto& p : kSc1)
+    if (p[0] == K && p[1] == M) return kFormPassSc1;
+  for (const auto& p : kPass)
+    if (p[0] == K && p[1] == M) return kFormPass;
+  return kFormLanes;
+}
+
+template <int K, int M, int FORM, bool PASSES>
 __global__ void __launch_bounds__((flat_block<K, M>())) rs_kernel(const RsArgs<K, M> a) {
   constexpr int B = flat_block<K, M>();
   __shared__ PermTab tab[M][K];
@@ -57,16 +94,39 @@ __global__ void __launch_bounds__((flat_block<K, M>())) rs_kernel(const RsArgs<K
     for (int q = threadIdx.x; q < M * K; q += B) tab[q / K][q % K] = a.tab[q / K][q % K];
     __syncthreads();
   }
-  const uint64_t stride = (uint64_t)gridDim.x * B;
-  for (uint64_t idx = (uint64_t)blockIdx.x * B + threadIdx.x; idx < a.n16; idx += stride) {
-    uint4 x[K];
+  if constexpr (FORM == kFormLanes) {
+    const uint64_t stride = (uint64_t)gridDim.x * B;
+    for (uint64_t idx = (uint64_t)blockIdx.x * B + threadIdx.x; idx < a.n16; idx += stride) {
+      uint4 x[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + idx * 16);
-    uint32_t acc[M][4] = {};
-    gf_matvec16<K, M>(acc, x, tab);
+      for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + idx * 16);
+      uint32_t acc[M][4] = {};
+      gf_matvec16<K, M>(acc, x, tab);
 #pragma unroll
-    for (int i = 0; i < M; ++i)
-      store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      for (int i = 0; i < M; ++i)
+        store_stream(a.out[i] + idx * 16, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+  } else {
+    const uint64_t stride = PASSES ? (uint64_t)gridDim.x * B : 0;
+    for (uint64_t base = (uint64_t)blockIdx.x * B; base < a.n16; base += stride) {
+      if (base + threadIdx.x < a.n16) {
+        const uint32_t lane = threadIdx.x * 16u;
+        uint4 x[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + base * 16 + lane);
+        uint32_t acc[M][4] = {};
+        gf_matvec16<K, M>(acc, x, tab);
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+          const uint4 v = make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+          if constexpr (FORM == kFormPassSc1)
+            store_wave<kPolicyNt | kPolicySc1>(a.out[i] + base * 16, lane, v);
+          else
+            store_stream(a.out[i] + base * 16 + lane, v);
+        }
+      }
+      if (!PASSES) break;
+    }
   }
 }
 
@@ -84,35 +144,39 @@ __device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uin
                     xor3(a.w, b.w, c.w));
 }
 
-// XOR parity: one-wavefront workgroups in launch order, one chunk per lane.
-// Measured on MI355X for XOR(4) (HBM traffic, GB/s): over 64 MiB shards 6482
-// vs 6357 for the former 512-lane workgroups with two chunks per lane (6399
-// with 128 lanes, 6288 with 256); over 256 MiB 6621 vs 6555.  The parity
-// store is a plain one for k > 1: XOR(4) 6470 against 6360 with a streaming
-// store over 64 MiB shards, 6806 against 6443 over 256 MiB.  rs_kernel is the
-// other way round (RS(6,3) over 256 MiB shards: streaming parity stores 0.80
-// of the roofline, plain 0.76), and so is the copy (k = 1, 3 % faster
-// streaming).
+// XOR parity: one-wavefront workgroups in launch order, one chunk per lane,
+// buffer loads on the workgroup's uniform base as in rs_kernel.  Measured on
+// MI355X for XOR(4) (HBM traffic, GB/s): over 64 MiB shards 6482 vs 6357 for
+// the former 512-lane workgroups with two chunks per lane (6399 with 128
+// lanes, 6288 with 256); over 256 MiB 6621 vs 6555.  The parity store of
+// k > 1 is an sc1 buffer store: XOR(4) over 4 x 64 MiB 50.9 us against 52.7
+// with a plain global store and 55.0 with an nt+sc1 one (same box, global
+// loads); a plain store had beaten a streaming one (6470 against 6360 GB/s).
+// The copy (k = 1) keeps the streaming global store, whose measured
+// alternatives were within 1 %.
 constexpr int kXorBlock = 64;
 
-template <int K>
+template <int K, bool PASSES>
 __global__ void __launch_bounds__(kXorBlock) xor_kernel(const XorArgs<K> a) {
-  const uint64_t stride = (uint64_t)gridDim.x * kXorBlock;
-  for (uint64_t idx = (uint64_t)blockIdx.x * kXorBlock + threadIdx.x; idx < a.n16;
-       idx += stride) {
-    uint4 x[K];
+  const uint64_t stride = PASSES ? (uint64_t)gridDim.x * kXorBlock : 0;
+  for (uint64_t base = (uint64_t)blockIdx.x * kXorBlock; base < a.n16; base += stride) {
+    if (base + threadIdx.x < a.n16) {
+      const uint32_t lane = threadIdx.x * 16u;
+      uint4 x[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) x[j] = load_stream(a.data[j] + idx * 16);
-    uint4 acc = x[0];
-    int j = 1;
+      for (int j = 0; j < K; ++j) x[j] = load_wave(a.data[j] + base * 16, lane);
+      uint4 acc = x[0];
+      int j = 1;
 #pragma unroll
-    for (; j + 1 < K; j += 2) acc = xor3v(acc, x[j], x[j + 1]);
-    if (j < K)
-      acc = make_uint4(acc.x ^ x[j].x, acc.y ^ x[j].y, acc.z ^ x[j].z, acc.w ^ x[j].w);
-    if (K == 1)  // a plain copy: streaming stores measured 3 % faster
-      store_stream(a.out + idx * 16, acc);
-    else
-      reinterpret_cast<uint4*>(a.out)[idx] = acc;
+      for (; j + 1 < K; j += 2) acc = xor3v(acc, x[j], x[j + 1]);
+      if (j < K)
+        acc = make_uint4(acc.x ^ x[j].x, acc.y ^ x[j].y, acc.z ^ x[j].z, acc.w ^ x[j].w);
+      if (K == 1)
+        store_stream(a.out + base * 16 + lane, acc);
+      else
+        store_wave<kPolicySc1>(a.out + base * 16, lane, acc);
+    }
+    if (!PASSES) break;
   }
 }
 
@@ -238,7 +302,16 @@ int launch_rs(const uint8_t* coeff, const uint8_t* const* d, uint8_t* const* o, 
     for (int j = 0; j < K; ++j) a.tab[i][j] = perm_tab(coeff[i * K + j]);
   a.n16 = n16;
   constexpr int B = flat_block<K, M>();
-  hipLaunchKernelGGL((rs_kernel<K, M>), dim3(grid_of(n16, B)), dim3(B), 0, st, a);
+  constexpr int F = flat_form<K, M>();
+  const unsigned grid = grid_of(n16, B);
+  if constexpr (F == kFormLanes) {
+    hipLaunchKernelGGL((rs_kernel<K, M, F, false>), dim3(grid), dim3(B), 0, st, a);
+  } else {
+    if ((uint64_t)grid * B >= n16)
+      hipLaunchKernelGGL((rs_kernel<K, M, F, false>), dim3(grid), dim3(B), 0, st, a);
+    else
+      hipLaunchKernelGGL((rs_kernel<K, M, F, true>), dim3(grid), dim3(B), 0, st, a);
+  }
   return hip_status();
 }
 
@@ -261,7 +334,11 @@ int launch_xor(const uint8_t* const* d, uint8_t* o, uint64_t n16, hipStream_t st
   for (int j = 0; j < K; ++j) a.data[j] = d[j];
   a.out = o;
   a.n16 = n16;
-  hipLaunchKernelGGL((xor_kernel<K>), dim3(grid_of(n16, kXorBlock)), dim3(kXorBlock), 0, st, a);
+  const unsigned grid = grid_of(n16, kXorBlock);
+  if ((uint64_t)grid * kXorBlock >= n16)
+    hipLaunchKernelGGL((xor_kernel<K, false>), dim3(grid), dim3(kXorBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((xor_kernel<K, true>), dim3(grid), dim3(kXorBlock), 0, st, a);
   return hip_status();
 }
 

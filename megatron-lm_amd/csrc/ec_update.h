@@ -43,7 +43,10 @@ struct UpdateArgs {
 // delta), then each changed unit's new and old chunks, so a lane has
 // U * (M + 2) loads in flight.  Misaligned units (views at arbitrary
 // offsets) are realigned there (load_realign); the aligned case keeps plain
-// loads (realigning every load cost the 1 % update 5 %).  Any other tile
+// loads (realigning every load cost the 1 % update 5 %).  The parity
+// stores are nt+sc1 buffer stores on the tile's wave-uniform base
+// (store_wave): config 5's 1 % update 310.9 -> 304.9 us against global nt
+// stores, same box; buffer loads as well measured 312.6.  Any other tile
 // takes the byte-granular path one chunk at a time.  Parity chunks that
 // start at or past the end of the stripe's longest changed unit are neither
 // read nor written: the delta is zero there.
@@ -135,9 +138,10 @@ __global__ void __launch_bounds__(B) update_kernel(const UpdateArgs<K, M> a) {
       for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int i = 0; i < M; ++i)
-          store_stream(p[i] + lo + (u * B + threadIdx.x) * 16u,
-                       make_uint4(pv[u][i].x ^ acc[u][i][0], pv[u][i].y ^ acc[u][i][1],
-                                  pv[u][i].z ^ acc[u][i][2], pv[u][i].w ^ acc[u][i][3]));
+          store_wave<kPolicyNt | kPolicySc1>(
+              p[i] + lo, (u * B + threadIdx.x) * 16u,
+              make_uint4(pv[u][i].x ^ acc[u][i][0], pv[u][i].y ^ acc[u][i][1],
+                         pv[u][i].z ^ acc[u][i][2], pv[u][i].w ^ acc[u][i][3]));
       continue;
     }
     // edge tile: a changed unit ends inside it or before it, or the parity

@@ -1011,7 +1011,11 @@ def test_flat_kernels_past_the_grid_cap(pkg, dev):
     """Shards of 16 GiB + 4 KiB + 48 B: more 16-byte chunks than the flat
     kernels' one-pass grid covers (2^24 one-wavefront workgroups), so the
     grid-stride loop runs a second time for the last chunks, and a byte tail
-    follows.  XOR(2) and RS(2,1) with unit coefficients both equal a ^ b."""
+    follows.  XOR(2) and RS(2,1) with unit coefficients both equal a ^ b
+    (XOR's wave-uniform loop, RS(2,1)'s per-lane loop); RS(4,1) over
+    [a, b, a, b] with coefficients (1, 1, 1, 0) equals b and RS(1,1) with
+    coefficient 1 equals a (the wave-uniform loop of the two pass forms of
+    rs_kernel, global and sc1 stores)."""
     n = (16 << 30) + 4096 + 48
     g = torch.Generator(device=dev)
     g.manual_seed(21)
@@ -1025,7 +1029,15 @@ def test_flat_kernels_past_the_grid_cap(pkg, dev):
     r = pkg.matvec(np.ones((1, 2), np.uint8), [a, b])[0]
     torch.cuda.synchronize()
     assert torch.equal(r, want)
-    del a, b, r, want
+    del r, want
+    r = pkg.matvec(np.array([[1, 1, 1, 0]], np.uint8), [a, b, a, b])[0]
+    torch.cuda.synchronize()
+    assert torch.equal(r, b)
+    del r
+    r = pkg.matvec(np.ones((1, 1), np.uint8), [a])[0]
+    torch.cuda.synchronize()
+    assert torch.equal(r, a)
+    del a, b, r
     torch.cuda.empty_cache()
 
 
