@@ -145,15 +145,17 @@ __device__ __forceinline__ uint4 xor3v(const uint4& a, const uint4& b, const uin
 }
 
 // XOR parity: one-wavefront workgroups in launch order, one chunk per lane,
-// buffer loads on the workgroup's uniform base as in rs_kernel.  Measured on
-// MI355X for XOR(4) (HBM traffic, GB/s): over 64 MiB shards 6482 vs 6357 for
-// the former 512-lane workgroups with two chunks per lane (6399 with 128
-// lanes, 6288 with 256); over 256 MiB 6621 vs 6555.  The parity store of
-// k > 1 is an sc1 buffer store: XOR(4) over 4 x 64 MiB 50.9 us against 52.7
-// with a plain global store and 55.0 with an nt+sc1 one (same box, global
-// loads); a plain store had beaten a streaming one (6470 against 6360 GB/s).
-// The copy (k = 1) keeps the streaming global store, whose measured
-// alternatives were within 1 %.
+// nt buffer loads on the workgroup's wave-uniform base (as the pass forms of
+// rs_kernel address it).  Measured on MI355X for XOR(4) (HBM traffic, GB/s):
+// over 64 MiB shards 6482 vs 6357 for the former 512-lane workgroups with two
+// chunks per lane (6399 with 128 lanes, 6288 with 256); over 256 MiB 6621 vs
+// 6555.  The parity store of k > 1 is an sc1 buffer store.  XOR(4) over
+// 4 x 64 MiB, same box: global nt loads with a plain global store 52.7 us,
+// with an sc1 buffer store 50.9, nt buffer loads with the sc1 buffer store
+// 48.9; on another box nt+sc1 stores took 54.8 us against 50.5 for sc1 ones
+// (a plain store had beaten a streaming one: 6470 against 6360 GB/s).  The
+// copy (k = 1) keeps the streaming global store, whose measured alternatives
+// were within 1 %.
 constexpr int kXorBlock = 64;
 
 template <int K, bool PASSES>

@@ -2,13 +2,15 @@
 // ceiling of the RS kernels' access pattern on the box it runs on.  Not part
 // of the C ABI of ec_mi355.h and not used by the product path.
 //
-// probe_kernel<R, W> is the memory skeleton of RS(6,3)'s rs_kernel: one-wave
-// (64-lane) workgroups in launch order, one 16-byte non-temporal load per
-// lane from each of R streams at the same column, and one non-temporal store
-// to each of W streams; the GF(2^8) arithmetic is replaced by one XOR.  With W = 0
-// the XOR result is stored to a 16-byte sink only if all four words equal a
-// value no data hits in practice, which keeps the loads alive; the sink is a
-// valid buffer either way.
+// probe_kernel<R, W> is the memory skeleton of RS(6,3)'s rs_kernel in the
+// form the library runs it: one-wave (64-lane) workgroups in launch order,
+// each on the 64 chunks at a wave-uniform base, one 16-byte global
+// non-temporal load per lane from each of R streams at the same column, and
+// one nt+sc1 buffer store on that base to each of W streams; the GF(2^8)
+// arithmetic is replaced by one XOR.  With W = 0 the XOR result is stored to
+// a 16-byte sink only if all four words equal a value no data hits in
+// practice, which keeps the loads alive; the sink is a valid buffer either
+// way.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -26,6 +28,13 @@ __device__ __forceinline__ u32x4 load_nt(const uint8_t* p) {
 __device__ __forceinline__ void store_nt(uint8_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, (global_u32x4*)(uintptr_t)p);
 }
+// 16-byte nt+sc1 (policy bits 2 | 16) buffer store at wave_base + lane_off,
+// wave_base the same for every lane of the wavefront.
+__device__ __forceinline__ void store_wave_ntsc1(uint8_t* wave_base, uint32_t lane_off, u32x4 v) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(wave_base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, lane_off, 0, 2 | 16);
+}
 
 struct ProbeArgs {
   const uint8_t* src[kMaxStreams];
@@ -37,17 +46,20 @@ struct ProbeArgs {
 template <int R, int W>
 __global__ void __launch_bounds__(kBlock) probe_kernel(const ProbeArgs a) {
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
-  for (uint64_t idx = (uint64_t)blockIdx.x * kBlock + threadIdx.x; idx < a.n16; idx += stride) {
+  for (uint64_t base = (uint64_t)blockIdx.x * kBlock; base < a.n16; base += stride) {
+    const uint64_t idx = base + threadIdx.x;
+    if (idx >= a.n16) break;
+    const uint32_t lane = threadIdx.x * 16u;
     u32x4 acc = {(uint32_t)idx, 0x9e3779b9u, 0x7f4a7c15u, 0x85ebca6bu};
 #pragma unroll
-    for (int j = 0; j < R; ++j) acc ^= load_nt(a.src[j] + idx * 16);
+    for (int j = 0; j < R; ++j) acc ^= load_nt(a.src[j] + base * 16 + lane);
     if constexpr (W == 0) {
       if (acc.x == 0xa5a5a5a5u && acc.y == 0xa5a5a5a5u && acc.z == 0xa5a5a5a5u &&
           acc.w == 0xa5a5a5a5u)
         store_nt(a.sink, acc);
     } else {
 #pragma unroll
-      for (int i = 0; i < W; ++i) store_nt(a.dst[i] + idx * 16, acc);
+      for (int i = 0; i < W; ++i) store_wave_ntsc1(a.dst[i] + base * 16, lane, acc);
     }
   }
 }
