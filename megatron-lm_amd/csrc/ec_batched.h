@@ -56,21 +56,34 @@ struct BatchArgs {
 // B * U <= 1024.)
 __device__ __align__(16) uint8_t g_zero_tile[1024 * 16] = {0};
 
-// Store of 16 bytes at base + rel for tile_full (base wave-uniform).
+// Where tile_full's stores of outputs that ended before the tile point
+// (their stores are dropped by the range check of store_wave_if, so nothing
+// is written; a valid address all the same).
+__device__ __align__(16) uint8_t g_sink_tile[1024 * 16];
+
+// Store of 16 bytes at base + rel for tile_full (base wave-uniform); with
+// WAVE a store with keep false is dropped (store_wave_if).
 template <bool WAVE>
-__device__ __forceinline__ void tile_store(uint8_t* base, uint32_t rel, const uint4& v) {
+__device__ __forceinline__ void tile_store(uint8_t* base, uint32_t rel, const uint4& v,
+                                           bool keep = true) {
   if constexpr (WAVE)
-    store_wave<kPolicyNt | kPolicySc1>(base, rel, v);
+    store_wave_if<kPolicyNt | kPolicySc1>(base, rel, v, keep);
   else
     store_stream(base + rel, v);
 }
 
-// One tile of a stripe in which no unit ends strictly inside the tile and
-// every output covers it (almost every tile).  src[j] points at the tile's
-// first byte of unit j, or at g_zero_tile if the unit ended before the tile;
-// dst[i] at the tile's first byte of output i.  (A branch around each store
-// for outputs that ended early triples the register count, so such tiles
-// take the edge path instead.)
+// One tile of a stripe in which no unit ends strictly inside the tile
+// (almost every tile).  src[j] points at the tile's first byte of unit j, or
+// at g_zero_tile if the unit ended before the tile; dst[i] at the tile's
+// first byte of output i.  Without WAVE every output covers the tile (a
+// branch around each store for outputs that ended early triples the register
+// count, so such tiles take the edge path).  With WAVE an output that ended
+// at or before the tile's start (a short data unit rebuilt by a decode) has
+// bit i of keep clear and its stores are dropped by the buffer range check:
+// 1 % of config 5's decode tiles, which took the byte-granular edge path
+// (same box, us per launch: lost data positions 0-3, 987 of them short,
+// 4177 -> 4140; the bench's 1, 7, 12, 14 4326 -> 4333, unchanged within the
+// noise).
 //
 // With COPY, cpy[j] points at the tile's first byte of unit j's copy (null:
 // no copy) and the loaded chunk is stored there too: the data is read once
@@ -90,7 +103,7 @@ __device__ __forceinline__ void tile_store(uint8_t* base, uint32_t rel, const ui
 template <int K, int M, int U, bool COPY, int B, bool WAVE>
 __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_t* const (&dst)[M],
                                           uint8_t* const (&cpy)[K],
-                                          const PermTab (&tab)[M][K]) {
+                                          const PermTab (&tab)[M][K], uint32_t keep = ~0u) {
   static_assert(B * U * 16 <= sizeof(g_zero_tile), "tile larger than the zero tile");
   uint4 x[U][K];
 #pragma unroll
@@ -107,7 +120,8 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
     gf_matvec16<K, M>(acc, x[u], tab);
 #pragma unroll
     for (int i = 0; i < M; ++i)
-      tile_store<WAVE>(dst[i], rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+      tile_store<WAVE>(dst[i], rel, make_uint4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]),
+                       (keep >> i) & 1u);
     if constexpr (COPY) {
 #pragma unroll
       for (int j = 0; j < K; ++j)
@@ -293,15 +307,25 @@ __device__ __forceinline__ void code_tile(const BatchArgs<K, M>& a, uint32_t s, 
     cpy[j] = st.c[j] ? st.c[j] + lo : nullptr;
     if (COPY) edge |= st.c[j] && a.unit_bytes < hi;  // a copy always spans the unit
   }
+  // With WAVE an output that ended at or before lo is dropped from the full
+  // path (keep); only an output ending strictly inside the tile makes it an
+  // edge tile.  The realigning path has no dropped stores: there any output
+  // short of hi makes an edge tile, as without WAVE.
+  uint32_t keep = 0;
+  bool short_out = false;
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    dst[i] = st.p[i] + lo;
-    edge |= st.olen[i] < hi;
+    const bool covers = st.olen[i] >= hi;
+    dst[i] = covers ? st.p[i] + lo : g_sink_tile;
+    keep |= (uint32_t)covers << i;
+    short_out |= !covers;
+    edge |= st.olen[i] > lo && st.olen[i] < hi;
   }
+  if (!WAVE || !st.in_aligned) edge |= short_out;
   if (edge)
     tile_edge<K, M, U, COPY, B>(a, s, base, tab);
   else if (st.in_aligned)
-    tile_full<K, M, U, COPY, B, WAVE>(src, dst, cpy, tab);
+    tile_full<K, M, U, COPY, B, WAVE>(src, dst, cpy, tab, keep);
   else
     tile_full_realign<K, M, U, COPY, B>(src, dst, cpy, tab);
 }

@@ -161,6 +161,19 @@ __device__ __forceinline__ void store_wave(void* base, uint32_t lane_off, const 
   __builtin_amdgcn_raw_buffer_store_b128(w, wave_rsrc(base), lane_off, 0, POLICY);
 }
 
+// store_wave when keep, else nothing, without a branch: the descriptor's
+// num_records is 0 when !keep, and the buffer unit's range check drops a
+// store whose offset is at or past num_records before it reaches memory.
+// keep must be wave-uniform, as base is.
+template <int POLICY>
+__device__ __forceinline__ void store_wave_if(void* base, uint32_t lane_off, const uint4& v,
+                                              bool keep) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(base, 0, keep ? 0x7fffffff : 0, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, lane_off, 0, POLICY);
+}
+
 // Copy the m x k permute tables from the kernel arguments into LDS, where
 // the unrolled loops read them as wave-uniform broadcasts straight into
 // VGPRs (v_perm_b32 may read only one SGPR, so tables held in SGPRs cost a
