@@ -12,10 +12,13 @@
 //   lane are all in flight together.  The m parity outputs of those bytes are
 //   accumulated in VGPRs and written once: every input byte is read from HBM
 //   exactly once and every parity byte written exactly once.  Loads and
-//   stores are non-temporal (streamed past L2 and the Infinity Cache).  The
-//   flat kernels run 64- or 128-lane workgroups in launch order
-//   (flat_block in ec_flat.hip); the kernels with k at run time and the
-//   batched ones 256-lane workgroups.  Measured on MI355X for RS(6,3) over
+//   stores are non-temporal (streamed past L2 and the Infinity Cache); some
+//   kernels issue them as buffer instructions on a wave-uniform base
+//   (load_wave, store_wave below).  The flat kernels run 64- or 128-lane
+//   workgroups in launch order (flat_block in ec_flat.hip), the fixed-size
+//   batched kernels and the update one-wavefront workgroups on 1 KiB tiles,
+//   the kernels with k at run time 64- to 256-lane workgroups.  Measured on
+//   MI355X for RS(6,3) over
 //   256 MiB shards (HBM traffic): plain loads/stores and tables in SGPRs
 //   5.48 TB/s; streaming access 5.90; plus LDS tables 6.15; 256-lane
 //   workgroups streaming each shard at two places (even XCDs the first
