@@ -12,9 +12,9 @@ namespace {
 // ------------------------------------------------ batched stripe kernels --
 // One workgroup per span of tiles (n_stripes x blocks_per_unit spans),
 // stripe-major: in launch order consecutive workgroups stream adjacent bytes
-// of the same k units; units of kSliceMinUnit and more are dealt in 8
-// interleaved slices instead (SpanGrid), except where the launcher splits the
-// launch in two (RS(8,2), see split_pays).  The descriptor of a stripe is uniform
+// of the same k units; units of kSliceMinUnit and more are dealt in 2 or 8
+// interleaved slices instead (SpanGrid, slice_shift_for), except where the
+// launcher splits the launch in two (RS(8,2), see split_pays).  The descriptor of a stripe is uniform
 // across the workgroup (scalar loads).
 //
 // The product launches one-wavefront workgroups with one 16-byte chunk per
@@ -539,7 +539,7 @@ int launch_batched_u(const uint8_t* coeff, const uint64_t* dptr, const uint32_t*
   const bool split = !COPY && U == 1 && split_pays<K, M>() && a.tiles_per_block == 1 &&
                      unit_bytes >= kSplitMinUnit && unit_bytes < kSplitMaxUnit;
   const uint64_t blocks = span_grid(a.grid, (uint64_t)n_stripes * a.blocks_per_unit,
-                                    split ? 0u : slice_shift_for(unit_bytes));
+                                    split ? 0u : slice_shift_for(unit_bytes, COPY));
   if (blocks == 0) return EC_ERANGE;
   if constexpr (!COPY && U == 1 && split_pays<K, M>()) {
     if (split) {

@@ -405,19 +405,30 @@ inline unsigned grid_of(uint64_t n16, int lanes) {
 // ----------------------------------------- grid order of batched launches --
 // A batched launch codes n_spans spans (a span: consecutive tiles of one
 // stripe, one workgroup each), stripe-major.  Units of kSliceMinUnit and
-// more are walked in 8 (2^kSliceShift) interleaved slices: the dispatcher deals
-// consecutive workgroups to the 8 XCDs in turn, so workgroup b taking span
-// (b % 8) * slice_spans + b / 8 makes each XCD stream its own eighth of the
-// stripes, and the work in flight sits at 8 unrelated offsets of the units
-// instead of one.  With large units the units a workgroup reads lie a unit
-// apart, and in launch order every workgroup in flight reads the same narrow
-// band of offsets of them.  Measured on MI355X (RS(8,2) encode over 20.8 GB,
-// fraction of the 8 TB/s roofline, launch order -> 8 slices): 2 MiB units
-// 0.741 -> 0.750, 4 MiB 0.723 -> 0.736, 8 MiB 0.691 -> 0.736, 16 MiB 0.584
-// -> 0.700, 32 MiB 0.621 -> 0.720, 64 MiB 0.685 -> 0.724; below 2 MiB the
-// slices cost 2-5 % (1 MiB 0.776 -> 0.734), and 64 KiB units gained nothing.
+// more are walked in interleaved slices: with 2^s slices, workgroup b takes
+// span (b mod 2^s) * slice_spans + b / 2^s, and the dispatcher deals
+// consecutive workgroups to the 8 XCDs in turn, so the work in flight sits
+// at 2^s unrelated offsets of the units instead of one (8 slices: each XCD
+// streams its own eighth of the stripes).  With large units the units a
+// workgroup reads lie a unit apart, and in launch order every workgroup in
+// flight reads the same narrow band of offsets of them.  Measured on MI355X,
+// fraction of the 8 TB/s roofline over one 20.8 GB buffer, single kernel,
+// launch order / 2 / 4 / 8 slices, two boxes alike:
+//   RS(12,4)  2 MiB 0.751 0.774 0.754 0.769    RS(6,3)  2 MiB 0.817 0.827 0.802 0.804
+//   RS(12,4)  4 MiB 0.719 0.759 0.731 0.747    RS(6,3)  4 MiB 0.779 0.799 0.775 0.776
+//   RS(12,4)  8 MiB 0.642 0.694 0.700 0.733    RS(6,3)  8 MiB 0.722 0.752 0.750 0.760
+//   RS(12,4) 16 MiB 0.534 0.602 0.646 0.717    RS(8,2) 32 MiB 0.648 0.748 0.773 0.785
+//   RS(12,4)  1 MiB 0.805 0.775 0.751 0.767 (launch order below 2 MiB)
+//   RS(4,2)   4 MiB 0.817 0.823   -   0.789    RS(4,2)  2 MiB 0.839 0.849   -   0.827
+// so an encode or decode over units of 2 MiB up to 8 MiB takes 2 slices and
+// over larger ones 8.  The copying encode keeps 8 slices from 2 MiB up: its
+// best order varied by code (RS(4,2) 4 MiB 0.744 0.715 - 0.726, RS(12,4)
+// 4 MiB 0.645 0.672 - 0.754, RS(4,2) 2 MiB 0.776 0.781 - 0.772).  (Before
+// the batched kernel's buffer accesses, 8 slices had measured best from
+// 2 MiB up: RS(8,2) 2 MiB 0.741 -> 0.750, 4 MiB 0.723 -> 0.736, 8 MiB 0.691
+// -> 0.736, 16 MiB 0.584 -> 0.700, 32 MiB 0.621 -> 0.720.)
 constexpr uint32_t kSliceMinUnit = 2u << 20;
-constexpr uint32_t kSliceShift = 3;  // kSlices = 8
+constexpr uint32_t kSliceWideUnit = 8u << 20;
 
 struct SpanGrid {
   uint32_t n_spans;      // the spans to code
@@ -425,8 +436,9 @@ struct SpanGrid {
   uint32_t slice_spans;  // ceil(n_spans / slices)
 };
 
-inline uint32_t slice_shift_for(uint32_t unit_bytes) {
-  return unit_bytes >= kSliceMinUnit ? kSliceShift : 0u;
+inline uint32_t slice_shift_for(uint32_t unit_bytes, bool copy) {
+  if (unit_bytes < kSliceMinUnit) return 0u;
+  return copy || unit_bytes >= kSliceWideUnit ? 3u : 1u;
 }
 
 // Fills g for `spans` (>= 1) spans in 2^shift slices and returns the grid,
