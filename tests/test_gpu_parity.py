@@ -398,13 +398,15 @@ def test_batched_decode_stripe_subset(pkg, dev):
 @pytest.mark.parametrize("k,m,unit,misalign,lost", [
     ((6, 3, (2 << 20) + 1024, False, (0, 4, 7))),   # 2049 tiles a unit: spans not a multiple of 8
     ((12, 4, (2 << 20) + 16, True, (1, 12))),       # realigned inputs, a 16-byte tail tile
-    ((8, 2, 4 << 20, True, (3, 9)))])
+    ((8, 2, 4 << 20, True, (3, 9))),
+    ((4, 2, (8 << 20) + 4096, False, (1, 4)))])     # 8 slices for the encode and decode too
 def test_batched_sliced_order(pkg, dev, k, m, unit, misalign, lost):
-    """Units of 2 MiB and more are walked in 8 interleaved slices of the
-    grid (rounded up to whole slices; the workgroups past the last span do
-    nothing).  The encode equals the oracle's, the copying encode into a
-    stripe-major block writes the same parity and zero-padded copies, and
-    lost positions decode back."""
+    """Units of 2 MiB and more are walked in interleaved slices of the grid
+    (2 slices for an encode or decode over units below 8 MiB, else 8; the
+    copying encode in 8), rounded up to whole slices; the workgroups past
+    the last span do nothing.  The encode equals the oracle's, the copying
+    encode into a stripe-major block writes the same parity and zero-padded
+    copies, and lost positions decode back."""
     from megatron_lm_amd import _lib
     from megatron_lm_amd.checkpoint import GpuSliceCodec
     rng = np.random.default_rng(unit + k)
