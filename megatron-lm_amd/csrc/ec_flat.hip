@@ -71,8 +71,9 @@ enum FlatForm : int { kFormLanes = 0, kFormPass = 1, kFormPassSc1 = 2 };
 //                 RS(13,1) 0.989, RS(16,1) 0.960
 // kFormLanes was ahead for most codes with k >= 7 (by up to 3-4 %: RS(10,3)
 // 1.022 / 1.041 for the pass forms, RS(9,2) 1.025 / 1.029), and the rest lie
-// within 0.5 %.  The headline shape, RS(6,3) over 6 x 256 MiB, in the same
-// library on one box: 375.9 us (kFormLanes) against 371.2 (kFormPassSc1).
+// within 0.5 %.  The headline shape, RS(6,3) over 6 x 256 MiB, on one box:
+// 375.9 us in the former library (kFormLanes) against 371.2 in this one
+// (kFormPassSc1).
 template <int K, int M>
 constexpr int flat_form() {
   constexpr int kSc1[][2] = {{1, 1}, {1, 2}, {1, 3}, {4, 3}, {4, 4}, {5, 3}, {6, 3}};
