@@ -362,6 +362,41 @@ def test_batched_decode_round_trip(pkg, dev, k, m, unit, lost):
     assert torch.equal(pset.parity, par_ref)
 
 
+def test_manager_default_code_every_erasure_pattern(pkg, dev):
+    """The checkpoint manager's default code and unit (RS(4,2), 4 MiB units:
+    the 2-slice grid order) over ragged tensors at odd offsets of an arena
+    filled with 0xC3: the encode against the oracle, then every pattern of
+    one or two lost positions erased (junk written over them) and decoded
+    back, the other bytes of the arena untouched."""
+    k, m, unit = 4, 2, 4 << 20
+    rng = np.random.default_rng(42)
+    host, tensors = _ragged_device(rng, dev, 9, 3 * unit + 777, misalign=True)
+    pset = pkg.encode(tensors, k, m, unit)
+    lay = pset.layout
+    torch.cuda.synchronize()
+    assert np.array_equal(pset.parity.cpu().numpy(), _oracle_layout_parity(lay, host, unit))
+    par_ref = pset.parity.clone()
+    arena = tensors[0]._base if tensors[0]._base is not None else None
+    arena_ref = arena.clone() if arena is not None else None
+    patterns = [(p,) for p in range(k + m)] + list(itertools.combinations(range(k + m), 2))
+    for lost in patterns:
+        for s in range(lay.n_stripes):
+            for pos in lost:
+                u = s * k + pos
+                if pos < k and u < lay.n_units:
+                    lay.unit_view(u).fill_(0xA5)
+                elif pos >= k:
+                    pset.parity[s, pos - k].fill_(0x5A)
+        pkg.decode(pset, list(lost))
+        torch.cuda.synchronize()
+        assert torch.equal(pset.parity, par_ref), lost
+        if arena is not None:
+            assert torch.equal(arena, arena_ref), lost
+        else:
+            for h, t in zip(host, tensors):
+                assert np.array_equal(t.cpu().numpy(), h), lost
+
+
 def test_batched_decode_stripe_subset(pkg, dev):
     """Decoding a subset of stripes rebuilds exactly those stripes; stripe
     indices are checked on the host."""
