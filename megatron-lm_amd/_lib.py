@@ -13,7 +13,7 @@ import threading
 
 LIB_NAME = "libec_mi355.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EC_OK = 0
 EC_EINVAL = -1
@@ -51,12 +51,12 @@ EXPORTS = (
 
 class StageStats(ctypes.Structure):
     """ec_stage_stats: the timings of a staging call."""
-    _fields_ = [("chunks", ctypes.c_uint32), ("wall_s", ctypes.c_double),
+    _fields_ = [("chunks", ctypes.c_uint32), ("copy_engine", ctypes.c_uint32), ("wall_s", ctypes.c_double),
                 ("wait_s", ctypes.c_double), ("host_copy_s", ctypes.c_double),
                 ("max_wait_s", ctypes.c_double), ("device_s", ctypes.c_double)]
 
     def as_dict(self) -> dict:
-        return {name: round(getattr(self, name), 4) if name != "chunks" else self.chunks
+        return {name: round(getattr(self, name), 4) if name not in ("chunks", "copy_engine") else getattr(self, name)
                 for name, _ in self._fields_}
 
 

@@ -360,9 +360,10 @@ class GpuSliceCodec:
         are in host memory.  Each chunk is one copying-encode launch on torch's
         current stream (ordered after the work that produced the tensors) into
         a stripe-major (stripes, k + m, unit_bytes) device buffer, which
-        ``ec_stage_stripes_to_host`` then moves into the slice rows on an
-        ordinary stream.  Two buffers alternate: chunk n + 1 is coded while
-        chunk n is staged."""
+        ``ec_stage_stripes_to_host`` then moves into the slice rows (on a
+        copy engine, after the chunk's coding, which an ordinary stream
+        carries).  Two buffers alternate: chunk n + 1 is coded while chunk
+        n is staged."""
         from . import _lib
         from .codec import stream_handle
         k, m, U = self.k, self.m, self.unit_bytes
@@ -375,8 +376,7 @@ class GpuSliceCodec:
         out = self._host_out((k + m, S * U))
         rows = [out[p].ctypes.data for p in range(k + m)]
         with torch.cuda.device(dev):
-            # transfers on an ordinary stream (on the CU-masked side stream they
-            # held the host and slowed the kernels beside them)
+            # the staging follows xfer's work (a wait for the chunk's coding)
             comp, xfer = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
             bufs = [torch.empty((C, k + m, U), dtype=torch.uint8, device=dev) for _ in range(nb)]
             pp = [self._unit_ptrs(b, k, m) for b in bufs]
@@ -506,9 +506,9 @@ class GpuSliceCodec:
             out = self._host_out((k + m, S * U))
             pinned = torch.empty(min(2 * self.chunk_bytes, 2 * (k + m) * S * U),
                                  dtype=torch.uint8, pin_memory=True)
-            # The transfers go on an ordinary stream, after the coding, in one
-            # foreign call that holds no interpreter lock (on the CU-masked
-            # side stream they held the host and slowed training's kernels).
+            # One foreign call that holds no interpreter lock: it waits for
+            # xfer's work (the coding), then copies on an SDMA engine, which
+            # leaves training's hardware queue alone.
             with torch.cuda.device(dev):
                 xfer = torch.cuda.Stream(dev)
                 xfer.wait_event(coded)

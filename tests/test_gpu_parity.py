@@ -886,6 +886,44 @@ def test_stage_stripes_to_host(pkg, dev, stripes, positions, unit, pinned, threa
     if total >= 1 << 20:   # long enough for the timing events to tell apart
         assert st["device_s"] > 0
     assert 0 <= st["host_copy_s"] <= st["wall_s"] and st["max_wait_s"] <= st["wait_s"]
+    assert st["copy_engine"] == 1   # runtime-allocated block and pinned buffer
+
+
+@pytest.mark.parametrize("pageable", [False, True])
+def test_stage_stripes_to_host_follows_its_stream(pkg, dev, pageable):
+    """ec_stage_stripes_to_host after work on a stream other than torch's:
+    the bytes staged are those that work left.  With a pinned buffer the
+    copies run on an SDMA engine once the stream's work is done; with a
+    pageable one (memory the runtime did not allocate) they fall back to
+    HIP transfers on the stream.  Both give the rows exactly."""
+    from megatron_lm_amd import _lib
+    from megatron_lm_amd.codec import stream_handle
+    stripes, positions, unit, pinned = 257, 6, 12288 + 16, 3 << 20
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    block = torch.randint(0, 256, (stripes, positions, unit), dtype=torch.uint8, device=dev,
+                          generator=g)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(32):   # queued work the copy must wait for
+            block.add_(3)
+    rows = [np.full(stripes * unit, 0x77, np.uint8) for _ in range(positions)]
+    if pageable:
+        pin_buf = np.empty(pinned, np.uint8)
+        pin_ptr = pin_buf.ctypes.data
+    else:
+        pin_buf = torch.empty(pinned, dtype=torch.uint8, pin_memory=True)
+        pin_ptr = pin_buf.data_ptr()
+    _lib.check(_lib.lib().ec_stage_stripes_to_host(
+        block.data_ptr(), stripes, positions, unit, _lib.ptr_array([r.ctypes.data for r in rows]),
+        pin_ptr, pinned, 4, stream_handle(side, dev)), "ec_stage_stripes_to_host")
+    st = _lib.last_stage_stats()
+    assert st["copy_engine"] == (0 if pageable else 1)
+    side.synchronize()
+    want = block.cpu().numpy()
+    for p in range(positions):
+        assert np.array_equal(rows[p], want[:, p, :].reshape(-1)), p
 
 
 @pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [
