@@ -144,7 +144,7 @@ def test_device_entry_points_reject_bad_arguments(pkg):
 
 def test_stage_stats_struct_matches_the_header(pkg):
     """The ctypes mirror of ec_stage_stats has the header's fields, in order,
-    with the C layout (a uint32 then five doubles: 48 bytes), and a thread
+    with the C layout (two uint32 then five doubles: 48 bytes), and a thread
     that staged nothing reads zeros."""
     import ctypes
     import threading
@@ -158,8 +158,8 @@ def test_stage_stats_struct_matches_the_header(pkg):
     t = threading.Thread(target=lambda: got.update(pkg._lib.last_stage_stats()))
     t.start()
     t.join()
-    assert got == {"chunks": 0, "wall_s": 0.0, "wait_s": 0.0, "host_copy_s": 0.0,
-                   "max_wait_s": 0.0, "device_s": 0.0}
+    assert got == {"chunks": 0, "copy_engine": 0, "wall_s": 0.0, "wait_s": 0.0,
+                   "host_copy_s": 0.0, "max_wait_s": 0.0, "device_s": 0.0}
 
 
 def test_shard_binding_loads_and_checks_operands(pkg):
