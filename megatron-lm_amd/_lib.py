@@ -51,13 +51,14 @@ EXPORTS = (
 
 class StageStats(ctypes.Structure):
     """ec_stage_stats: the timings of a staging call."""
-    _fields_ = [("chunks", ctypes.c_uint32), ("copy_engine", ctypes.c_uint32), ("wall_s", ctypes.c_double),
-                ("wait_s", ctypes.c_double), ("host_copy_s", ctypes.c_double),
-                ("max_wait_s", ctypes.c_double), ("device_s", ctypes.c_double)]
+    _fields_ = [("chunks", ctypes.c_uint32), ("copy_engine", ctypes.c_uint32),
+                ("wall_s", ctypes.c_double), ("wait_s", ctypes.c_double),
+                ("host_copy_s", ctypes.c_double), ("max_wait_s", ctypes.c_double),
+                ("device_s", ctypes.c_double)]
 
     def as_dict(self) -> dict:
-        return {name: round(getattr(self, name), 4) if name not in ("chunks", "copy_engine") else getattr(self, name)
-                for name, _ in self._fields_}
+        return {name: getattr(self, name) if kind is ctypes.c_uint32 else round(getattr(self, name), 4)
+                for name, kind in self._fields_}
 
 
 def last_stage_stats() -> dict:
