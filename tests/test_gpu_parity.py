@@ -889,6 +889,31 @@ def test_stage_stripes_to_host(pkg, dev, stripes, positions, unit, pinned, threa
     assert st["copy_engine"] == 1   # runtime-allocated block and pinned buffer
 
 
+def test_stage_stripes_to_host_odd_addresses(pkg, dev):
+    """The copy-engine path with a block and a pinned buffer at odd
+    addresses inside larger allocations, odd units and an odd pinned size
+    (halves of 500 bytes): every byte lands in its row, nothing past a row's
+    end is written."""
+    from megatron_lm_amd import _lib
+    stripes, positions, unit = 37, 5, 1001
+    total = stripes * positions * unit
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    big = torch.randint(0, 256, (total + 64,), dtype=torch.uint8, device=dev, generator=g)
+    block = big[5: 5 + total]
+    rows = [np.full(stripes * unit + 16, 0x77, np.uint8) for _ in range(positions)]
+    pin = torch.empty(1024, dtype=torch.uint8, pin_memory=True)
+    _lib.check(_lib.lib().ec_stage_stripes_to_host(
+        block.data_ptr(), stripes, positions, unit, _lib.ptr_array([r.ctypes.data for r in rows]),
+        pin.data_ptr() + 3, 1001, 2, None), "ec_stage_stripes_to_host")
+    st = _lib.last_stage_stats()
+    assert st["copy_engine"] == 1 and st["chunks"] == -(-total // 500)
+    want = block.cpu().numpy().reshape(stripes, positions, unit)
+    for p in range(positions):
+        assert np.array_equal(rows[p][:stripes * unit], want[:, p, :].reshape(-1)), p
+        assert (rows[p][stripes * unit:] == 0x77).all(), p
+
+
 @pytest.mark.parametrize("pageable", [False, True])
 def test_stage_stripes_to_host_follows_its_stream(pkg, dev, pageable):
     """ec_stage_stripes_to_host after work on a stream other than torch's:
