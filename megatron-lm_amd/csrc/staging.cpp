@@ -139,13 +139,6 @@ uint64_t half_of(uint64_t pinned_bytes, uint64_t per_byte_rows) {
 
 // ---- Copies on an SDMA engine (ec_stage_stripes_to_host) ----
 
-// ROCr is the runtime under HIP and is open once HIP is; hsa_init takes
-// this library's own reference on it, once per process.
-bool hsa_ready() {
-  static const bool ok = hsa_init() == HSA_STATUS_SUCCESS;
-  return ok;
-}
-
 enum class Owner { kNone, kFits, kShort };
 
 // Where [p, p + bytes) lies: kFits when inside one allocation ROCr made
@@ -175,7 +168,10 @@ Owner owner_of(const void* p, uint64_t bytes, hsa_device_type_t type, hsa_agent_
 
 // Two completion signals (one per pinned half) and the engine chosen for
 // device-to-host copies; the signals are destroyed, after every copy has
-// landed, when it goes out of scope.
+// landed, when it goes out of scope.  ROCr, the runtime under HIP, is open
+// once HIP is (the Session's HIP calls come first); the library takes no
+// reference of its own on it, so its teardown at exit stays HIP's.  Were it
+// not open, the pointer queries fail and the call takes HIP transfers.
 struct EngineCopies {
   hsa_agent_t gpu = {0}, cpu = {0};
   hsa_amd_sdma_engine_id_t engine = HSA_AMD_SDMA_ENGINE_0;
@@ -189,7 +185,6 @@ struct EngineCopies {
   // EC_EINVAL when d_block's allocation ends before the block does.
   int setup(const uint8_t* d_block, uint64_t block_bytes, uint8_t* h_pinned,
             uint64_t pinned_bytes) {
-    if (!hsa_ready()) return EC_OK;
     const Owner dev = owner_of(d_block, block_bytes, HSA_DEVICE_TYPE_GPU, &gpu);
     if (dev == Owner::kShort) return EC_EINVAL;
     if (dev != Owner::kFits ||
