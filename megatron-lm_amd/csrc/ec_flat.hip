@@ -41,7 +41,10 @@ struct RsArgs {
 // (5657-6097 before).  Smaller workgroups also made the rate less dependent
 // on the box: the 256-lane kernel ran RS(6,3) at 393 to 424 us per launch on
 // three boxes, the 64/128-lane ones at 376 to 386.  The two-window order lost
-// with them (RS(6,3) one wave: 6202 vs 6404 at 256 MiB).
+// with them (RS(6,3) one wave: 6202 vs 6404 at 256 MiB), and so did
+// interleaved slices, workgroup b taking column (b mod 2^s) * ceil(n / 2^s) +
+// b / 2^s (RS(6,3) over 6 x 256 MiB, us per launch, one box: launch order
+// 373, 8 slices, one per XCD, 378-381, 32 slices 406, 256 slices 447).
 template <int K, int M>
 constexpr int flat_block() {
   return K * M <= 20 ? 64 : 128;
