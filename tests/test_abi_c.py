@@ -1,6 +1,7 @@
 """The C ABI from C: the header is strict C, and a plain-C program linked
 against libec_mi355.so encodes, reconstructs and XORs on the GPU, and codes a
-checkpoint snapshot and stages it to host memory."""
+checkpoint snapshot and stages it to host memory (row-major, then stripe-major on
+a copy engine)."""
 import os
 import subprocess
 
