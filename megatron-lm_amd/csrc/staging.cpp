@@ -19,8 +19,9 @@
 // CU-masked stream the HIP transfers also held the host; a copy kernel
 // writing the pinned buffer through its device address, on a stream of its
 // own, slowed training's steps by up to 2.3x, also on a few CUs.)  The
-// row-major calls serve the synchronous save and the load, which hold the
-// caller anyway, and keep HIP transfers on the caller's stream.
+// row-major ec_stage_to_host and the upload of the load path
+// (ec_stage_to_device), which holds its caller anyway, keep HIP transfers on
+// the caller's stream.
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
