@@ -250,18 +250,14 @@ int ec_stream_destroy(ec_stream_t stream);
  * one byte of every row per half; rows or row_bytes 0 is a no-op.  No
  * counterpart in the reference: its checkpoint D2H is
  * copy_tensors_to_cpu (tensor_aware_state_dict.py:245-274), run in the
- * training process before the async writer starts.  This call stages a
- * coded checkpoint in the background while training runs in the same
- * process, whole inside the library (a Python caller through ctypes holds
- * no interpreter lock meanwhile).  Pass an ordinary stream, not one from
- * ec_stream_create: measured on MI355X, transfers issued on a CU-masked
- * stream held the host and slowed the kernels beside them; on an ordinary
- * stream they ran asynchronously without doing so.  They run as the HIP
- * runtime's copy kernels on the stream's hardware queue, and the runtime
- * spreads streams over a few queues: when that queue is also the training
- * stream's, the copies run in order between training's kernels (6.44 GB
- * staged beside a training loop cost it 11 ms in one run and 46 ms in
- * another). */
+ * training process before the async writer starts.  The whole loop runs
+ * inside the library (a Python caller through ctypes holds no interpreter
+ * lock meanwhile).  Pass an ordinary stream, not one from ec_stream_create:
+ * measured on MI355X, transfers issued on a CU-masked stream held the host
+ * and slowed the kernels beside them.  The transfers run as the HIP
+ * runtime's copy kernels on the stream's hardware queue, which the runtime
+ * may share with the training stream: for a block staged beside training,
+ * ec_stage_stripes_to_host copies on an SDMA engine instead. */
 int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                      uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
                      uint64_t pinned_bytes, int threads, ec_stream_t stream);
