@@ -242,22 +242,25 @@ int ec_stream_destroy(ec_stream_t stream);
 /* Copies a rows x row_bytes region of device memory (row pitch src_pitch)
  * to host memory that need not be pinned (row pitch dst_pitch), through the
  * caller's pinned buffer h_pinned of pinned_bytes: the buffer's two halves
- * alternate, the transfer of one chunk of columns runs on `stream` while
- * `threads` host threads copy the previous chunk out of the other half.
- * Returns when every byte is in h_dst; the transfers follow the work
- * already enqueued on `stream`.  EC_EINVAL for null pointers, pitches below
- * row_bytes, threads outside [1, 64], or a pinned buffer without room for
- * one byte of every row per half; rows or row_bytes 0 is a no-op.  No
+ * alternate, the transfer of one chunk of columns (one copy per row) runs
+ * while `threads` host threads copy the previous chunk out of the other
+ * half.  Returns when every byte is in h_dst.  As in
+ * ec_stage_stripes_to_host, the copies run on an SDMA engine after the
+ * call has waited on the host for the work already enqueued on `stream`
+ * when d_src and h_pinned were allocated through the runtime
+ * (ec_stage_stats.copy_engine = 1), else as HIP transfers on `stream`,
+ * after its work.  EC_EINVAL for null pointers, pitches below
+ * row_bytes, threads outside [1, 64], a pinned buffer without room for one
+ * byte of every row per half, a region whose size overflows 64 bits, or a
+ * runtime allocation holding d_src that ends before the region does; rows
+ * or row_bytes 0 is a no-op.  No
  * counterpart in the reference: its checkpoint D2H is
  * copy_tensors_to_cpu (tensor_aware_state_dict.py:245-274), run in the
  * training process before the async writer starts.  The whole loop runs
  * inside the library (a Python caller through ctypes holds no interpreter
  * lock meanwhile).  Pass an ordinary stream, not one from ec_stream_create:
- * measured on MI355X, transfers issued on a CU-masked stream held the host
- * and slowed the kernels beside them.  The transfers run as the HIP
- * runtime's copy kernels on the stream's hardware queue, which the runtime
- * may share with the training stream: for a block staged beside training,
- * ec_stage_stripes_to_host copies on an SDMA engine instead. */
+ * measured on MI355X, HIP transfers issued on a CU-masked stream held the
+ * host and slowed the kernels beside them. */
 int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
                      uint64_t dst_pitch, uint32_t rows, uint64_t row_bytes, uint8_t* h_pinned,
                      uint64_t pinned_bytes, int threads, ec_stream_t stream);

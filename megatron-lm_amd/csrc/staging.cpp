@@ -200,13 +200,19 @@ struct EngineCopies {
     ready = true;
     return EC_OK;
   }
-  // Starts the copy of w bytes from src into dst, completing signal h.
-  bool start(int h, uint8_t* dst, const uint8_t* src, uint64_t w) {
-    hsa_signal_store_relaxed(sig[h], 1);
-    busy[h] = hsa_amd_memory_async_copy_on_engine(dst, cpu, src, gpu, w, 0, nullptr, sig[h],
-                                                  engine, true) == HSA_STATUS_SUCCESS;
-    return busy[h];
+  // Arms signal h for the n copies that fill pinned half h.
+  void arm(int h, uint32_t n) {
+    hsa_signal_store_relaxed(sig[h], n);
+    busy[h] = true;
   }
+  // Starts the copy of w bytes from src into dst; it completes on signal h
+  // (armed).  False if the runtime refused it: then forgo() the copies of
+  // the half that were never started.
+  bool copy(int h, uint8_t* dst, const uint8_t* src, uint64_t w) {
+    return hsa_amd_memory_async_copy_on_engine(dst, cpu, src, gpu, w, 0, nullptr, sig[h], engine,
+                                               true) == HSA_STATUS_SUCCESS;
+  }
+  void forgo(int h, uint32_t n) { hsa_signal_subtract_relaxed(sig[h], n); }
   // Blocks (asleep) until signal h's copy has landed.
   void wait(int h) {
     if (!busy[h]) return;
@@ -237,11 +243,53 @@ int ec_stage_to_host(const uint8_t* d_src, uint64_t src_pitch, uint8_t* h_dst,
   uint64_t width = half_of(pinned_bytes, rows);
   if (width == 0) return EC_EINVAL;
   width = std::min(width, row_bytes);
+  // The device region: rows - 1 pitches and one row.
+  if (rows > 1 && src_pitch > (UINT64_MAX - row_bytes) / (rows - 1)) return EC_EINVAL;
+  const uint64_t src_span = (uint64_t)(rows - 1) * src_pitch + row_bytes;
   Session ss(stream);
+  if (!ss.ok()) return ss.status;
+  EngineCopies eng;
+  const int st = eng.setup(d_src, src_span, h_pinned, 2 * half);
+  if (st != EC_OK) return st;
   const uint64_t n_chunks = (row_bytes + width - 1) / width;
   // Chunk j: columns [j * width, min(row_bytes, (j + 1) * width)) of every
   // row, through pinned half j % 2.  The transfer of chunk j is in flight
-  // while the threads copy chunk j - 1 out of the other half.
+  // while the threads copy chunk j - 1 out of the other half.  On a copy
+  // engine (as ec_stage_stripes_to_host) when both buffers allow it, else
+  // HIP transfers on the stream.
+  if (eng.ready) {
+    if (hipStreamSynchronize(ss.st) != hipSuccess) return EC_EHIP;
+    ss.stats.copy_engine = 1;
+    const Clock::time_point t_dev = Clock::now();
+    for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
+      if (j < n_chunks) {
+        const uint64_t x0 = j * width, w = std::min(width, row_bytes - x0);
+        const int h = (int)(j % 2);
+        uint8_t* pin = h_pinned + h * half;
+        eng.arm(h, rows);
+        for (uint32_t r = 0; r < rows; ++r)
+          if (!eng.copy(h, pin + (uint64_t)r * w, d_src + (uint64_t)r * src_pitch + x0, w)) {
+            eng.forgo(h, rows - r);
+            ss.fail();
+            break;
+          }
+        ++ss.stats.chunks;
+      }
+      if (j >= 1 && ss.ok()) {
+        const uint64_t p = j - 1, x0 = p * width, w = std::min(width, row_bytes - x0);
+        const Clock::time_point t0 = Clock::now();
+        eng.wait((int)(p % 2));
+        const double wt = seconds_since(t0);
+        ss.stats.wait_s += wt;
+        ss.stats.max_wait_s = std::max(ss.stats.max_wait_s, wt);
+        if (p + 1 == n_chunks) ss.stats.device_s = seconds_since(t_dev);
+        ss.host_copy([&] {
+          ec::copy_rect(h_dst + x0, dst_pitch, h_pinned + (p % 2) * half, w, rows, w, threads);
+        });
+      }
+    }
+    return ss.status;   // eng's destructor waits for copies still in flight
+  }
   ss.begin();
   for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
     if (j < n_chunks) {
@@ -298,7 +346,12 @@ int ec_stage_stripes_to_host(const uint8_t* d_block, uint32_t n_stripes, uint32_
     for (uint64_t j = 0; ss.ok() && j <= n_chunks; ++j) {
       if (j < n_chunks) {
         const uint64_t x0 = j * width, w = std::min(width, total - x0);
-        if (!eng.start((int)(j % 2), h_pinned + (j % 2) * half, d_block + x0, w)) ss.fail();
+        const int h = (int)(j % 2);
+        eng.arm(h, 1);
+        if (!eng.copy(h, h_pinned + h * half, d_block + x0, w)) {
+          eng.forgo(h, 1);
+          ss.fail();
+        }
         ++ss.stats.chunks;
       }
       if (j >= 1 && ss.ok()) {

@@ -824,25 +824,31 @@ def test_encode_batched_copy_every_instantiated_shape(pkg, dev, unit):
             assert np.array_equal(got[:k].transpose(1, 0, 2).reshape(-1), stream), (k, m)
 
 
-@pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads", [
-    (16, (1 << 20) + 48, (1 << 20) + 64, 1 << 20, 8),   # many chunks, a short last one
-    (3, 5000, 5000, 64, 1),                             # chunks narrower than a page
-    (1, 4096, 8192, 1 << 16, 64),                       # one row, more threads than bytes/64
+@pytest.mark.parametrize("rows,row_bytes,pitch,pinned,threads,pageable", [
+    (16, (1 << 20) + 48, (1 << 20) + 64, 1 << 20, 8, False),   # many chunks, a short last one
+    (3, 5000, 5000, 64, 1, False),                             # chunks narrower than a page
+    (1, 4096, 8192, 1 << 16, 64, False),                       # one row, more threads than bytes/64
+    (5, 70000, 70016, 1 << 16, 4, True),                       # HIP transfers: pageable "pinned"
 ])
-def test_stage_to_host(pkg, dev, rows, row_bytes, pitch, pinned, threads):
+def test_stage_to_host(pkg, dev, rows, row_bytes, pitch, pinned, threads, pageable):
     """ec_stage_to_host copies a pitched device region into pageable host
     memory exactly, through a pinned buffer smaller than the region, after
-    the work already on the stream."""
+    the work already on the stream: on a copy engine with a pinned buffer,
+    with HIP transfers when the buffer is memory the runtime did not
+    allocate."""
     from megatron_lm_amd import _lib
     g = torch.Generator(device=dev)
     g.manual_seed(rows)
     src = torch.randint(0, 256, (rows, pitch), dtype=torch.uint8, device=dev, generator=g)
     out = np.full((rows, pitch + 16), 0x77, np.uint8)
-    pin = torch.empty(pinned, dtype=torch.uint8, pin_memory=True)
+    pin = np.empty(pinned, np.uint8) if pageable else torch.empty(pinned, dtype=torch.uint8,
+                                                                  pin_memory=True)
+    pin_ptr = pin.ctypes.data if pageable else pin.data_ptr()
     src.add_(1)   # enqueued before the call: the copy must see it
     _lib.check(_lib.lib().ec_stage_to_host(
-        src.data_ptr(), pitch, out.ctypes.data, pitch + 16, rows, row_bytes, pin.data_ptr(),
+        src.data_ptr(), pitch, out.ctypes.data, pitch + 16, rows, row_bytes, pin_ptr,
         pinned, threads, None), "ec_stage_to_host")
+    assert _lib.last_stage_stats()["copy_engine"] == (0 if pageable else 1)
     want = src.cpu().numpy()
     assert np.array_equal(out[:, :row_bytes], want[:, :row_bytes])
     assert (out[:, row_bytes:] == 0x77).all()
