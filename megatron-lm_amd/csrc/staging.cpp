@@ -9,9 +9,9 @@
 // ctypes makes with the interpreter's lock released, so the staging thread
 // takes that lock from the training thread only to start and to finish.
 //
-// ec_stage_stripes_to_host moves the block with one of the GPU's SDMA copy
-// engines (the ROCr copy API, forced onto an engine), not with HIP
-// transfers.  HIP runs device-to-host transfers as copy kernels on the
+// The two device-to-host calls move their bytes with one of the GPU's SDMA
+// copy engines (the ROCr copy API, forced onto an engine), not with HIP
+// transfers, when both buffers are runtime allocations.  HIP runs device-to-host transfers as copy kernels on the
 // stream's hardware queue, and it spreads streams over a few queues: when
 // the staging stream's queue was training's, its 1 GiB copies ran in order
 // between training's kernels, and a save cost a training loop 6-91 ms
@@ -19,9 +19,8 @@
 // CU-masked stream the HIP transfers also held the host; a copy kernel
 // writing the pinned buffer through its device address, on a stream of its
 // own, slowed training's steps by up to 2.3x, also on a few CUs.)  The
-// row-major ec_stage_to_host and the upload of the load path
-// (ec_stage_to_device), which holds its caller anyway, keep HIP transfers on
-// the caller's stream.
+// upload of the load path (ec_stage_to_device), which holds its caller
+// anyway, keeps HIP transfers on the caller's stream.
 #include <hip/hip_runtime.h>
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
