@@ -920,6 +920,53 @@ def test_stage_stripes_to_host_odd_addresses(pkg, dev):
         assert (rows[p][stripes * unit:] == 0x77).all(), p
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_staging_random_shapes(pkg, dev, seed):
+    """Both device-to-host calls over seeded random shapes: block and region
+    at random byte offsets inside larger allocations, random units, pitches,
+    pinned sizes (halves from a few bytes to whole pages) and thread counts,
+    pinned or pageable buffers; every byte lands where it belongs and
+    nothing past a row's end is written."""
+    from megatron_lm_amd import _lib
+    rng = np.random.default_rng(100 + seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    stripes, positions = int(rng.integers(1, 40)), int(rng.integers(1, 17))
+    unit = int(rng.integers(1, 70000))
+    total = stripes * positions * unit
+    off = int(rng.integers(0, 64))
+    big = torch.randint(0, 256, (total + off + 64,), dtype=torch.uint8, device=dev, generator=g)
+    block = big[off: off + total]
+    pinned = int(rng.choice([int(rng.integers(2, 5000)), int(rng.integers(8192, 1 << 21))]))
+    pageable = bool(rng.integers(0, 2))
+    pin = np.empty(pinned + 7, np.uint8) if pageable else torch.empty(pinned + 7, dtype=torch.uint8,
+                                                                      pin_memory=True)
+    pin_ptr = (pin.ctypes.data if pageable else pin.data_ptr()) + int(rng.integers(0, 8))
+    threads = int(rng.integers(1, 9))
+    rows = [np.full(stripes * unit + 16, 0x77, np.uint8) for _ in range(positions)]
+    _lib.check(_lib.lib().ec_stage_stripes_to_host(
+        block.data_ptr(), stripes, positions, unit, _lib.ptr_array([r.ctypes.data for r in rows]),
+        pin_ptr, pinned, threads, None), "ec_stage_stripes_to_host")
+    assert _lib.last_stage_stats()["copy_engine"] == (0 if pageable else 1)
+    want = block.cpu().numpy().reshape(stripes, positions, unit)
+    for p in range(positions):
+        assert np.array_equal(rows[p][:stripes * unit], want[:, p, :].reshape(-1)), (seed, p)
+        assert (rows[p][stripes * unit:] == 0x77).all(), (seed, p)
+    # the same bytes as a pitched region: rows of row_bytes at a pitch of one
+    # unit (a pinned half holds at least one byte of every row)
+    n_rows = max(1, min(positions * stripes, int(rng.integers(1, 12)), pinned // 2))
+    row_bytes = int(rng.integers(1, unit + 1))
+    out = np.full((n_rows, row_bytes + 16), 0x77, np.uint8)
+    _lib.check(_lib.lib().ec_stage_to_host(
+        block.data_ptr(), unit, out.ctypes.data, row_bytes + 16, n_rows, row_bytes, pin_ptr,
+        pinned, threads, None), "ec_stage_to_host")
+    assert _lib.last_stage_stats()["copy_engine"] == (0 if pageable else 1)
+    flat = block.cpu().numpy()
+    for r in range(n_rows):
+        assert np.array_equal(out[r, :row_bytes], flat[r * unit: r * unit + row_bytes]), (seed, r)
+        assert (out[r, row_bytes:] == 0x77).all(), (seed, r)
+
+
 @pytest.mark.parametrize("pageable", [False, True])
 def test_stage_stripes_to_host_follows_its_stream(pkg, dev, pageable):
     """ec_stage_stripes_to_host after work on a stream other than torch's:
