@@ -48,8 +48,8 @@ extern "C" {
 
 /* 2: ec_stage_stripes_to_host added; the batched kernels read every
  * descriptor entry of a stripe, also the length of an absent unit.
- * 3: ec_stage_stripes_to_host copies on an SDMA engine (see there);
- * ec_stage_stats.copy_engine added. */
+ * 3: ec_stage_stripes_to_host and ec_stage_to_host copy on an SDMA engine
+ * (see there); ec_stage_stats.copy_engine added. */
 #define EC_ABI_VERSION 3
 
 /* Status codes. */
