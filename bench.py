@@ -433,6 +433,19 @@ def batched_configs(pkg, synth, dev, seed: int, gemm: "GemmLoad", cpu_seconds: f
     out["rs124_ragged_decode4_GBps"] = round(lay.data_bytes / (e * 1e-3) / 1e9, 1)
     out["rs124_ragged_decode4_traffic_GBps"] = round(dec_traffic / (e * 1e-3) / 1e9, 1)
     log(f"update {out['update_1pct_ms']} ms, decode {out['rs124_ragged_decode4_GBps']} GB/s")
+    # the same decode kernel by lost set: where the written units lie among the
+    # read ones sets the rate (parity only: the tensors are only read)
+    by_set = {}
+    for other in ([12, 13, 14, 15], [0, 1, 2, 3], [1, 7]):
+        oplan = lay.plan_decode(par, other)
+        _, eo = steady(lambda: lay.run(oplan), 5, 1)
+        osurv = [p for p in range(16) if p not in other][:k5]
+        otraffic = sum(int(hl[:, p].sum()) if p < k5 else S5 * U5 for p in osurv + other)
+        by_set[",".join(map(str, other))] = round(otraffic / (eo * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)
+        del oplan
+    by_set["1,7,12,14"] = round(dec_traffic / (e * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)
+    out["rs124_ragged_decode_frac_by_lost_set"] = by_set
+    log(f"decode, fraction of the roofline by lost set: {by_set}")
     if cpu_seconds:
         cpu["rs124_ragged_decode4"] = {
             **cpu_decode_batched(lay, views, lost, hptr, hlen, sample,
