@@ -132,8 +132,11 @@ __device__ __forceinline__ void tile_full(const uint8_t* const (&src)[K], uint8_
 
 // A full tile whose units are not all 16-byte aligned (tensors that are
 // views into a flat buffer at arbitrary offsets): one chunk per lane at a
-// time, each unit read through load_realign (two aligned loads and a byte
-// shift for a misaligned unit); the outputs are aligned.
+// time, each unit read through load_realign (one unaligned dwordx4 load for
+// a misaligned unit); the outputs are aligned.  A separate path from
+// tile_full on purpose: routing misaligned units through tile_full itself
+// (buffer loads at their byte addresses) changed the compiler's schedule of
+// the aligned path, config 5's encode 4145 -> 4250 us.
 template <int K, int M, int U, bool COPY, int B>
 __device__ __forceinline__ void tile_full_realign(const uint8_t* const (&src)[K],
                                                   uint8_t* const (&dst)[M],

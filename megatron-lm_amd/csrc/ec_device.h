@@ -313,32 +313,25 @@ constexpr int kWidePair() {
 
 // 16 bytes at base + off, where off is a multiple of 16 and base may have any
 // alignment r = base mod 16 (uniform: it depends on the shard only).  r = 0
-// is one dwordx4 load; otherwise the two aligned dwordx4 that hold the bytes
-// are loaded and v_alignbyte_b32 ({hi, lo} >> 8 * (byte count)) shifts them
-// into place.  Both aligned
-// blocks hold at least one byte of [base + off, base + off + 16), so no
-// load leaves the 16-byte blocks (and pages) that the shard itself touches.
-template <int Q>
-__device__ __forceinline__ uint4 align_words(const uint4& lo, const uint4& hi, uint32_t sh) {
-  const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-  return make_uint4(__builtin_amdgcn_alignbyte(w[Q + 1], w[Q], sh),
-                    __builtin_amdgcn_alignbyte(w[Q + 2], w[Q + 1], sh),
-                    __builtin_amdgcn_alignbyte(w[Q + 3], w[Q + 2], sh),
-                    __builtin_amdgcn_alignbyte(w[Q + 4], w[Q + 3], sh));
-}
+// is the aligned dwordx4 load; otherwise one dwordx4 load at the unaligned
+// address (the vector type below has alignment 1, so the compiler neither
+// splits the load nor assumes its alignment; the hardware takes unaligned
+// addresses), non-temporal like the aligned one.  It reads exactly the 16
+// bytes asked for.  Measured on MI355X against the former form (the two
+// aligned blocks holding the bytes, shifted into place with
+// v_alignbyte_b32), HBM traffic, TB/s, one box: 600 fp32 tensor views of one
+// flat buffer (6.82 GB, 450 of them misaligned) through the batched kernels,
+// RS(12,4) in 64 KiB units 4.66 -> 5.88, RS(8,2) in 4 MiB units 3.51 ->
+// 4.15, RS(6,3) in 1 MiB units 4.88 -> 5.94 (6.15-6.65 for aligned copies of
+// the same tensors); RS(6,3) over six 64 MiB shards at skews 1-6 through the
+// wide kernel 5.24 -> 5.62.  Aligned inputs do not take this path.
+typedef uint32_t u32x4_unaligned __attribute__((ext_vector_type(4), aligned(1)));
 
 __device__ __forceinline__ uint4 load_realign(const uint8_t* base, uint64_t off) {
-  const uint32_t r = (uint32_t)reinterpret_cast<uintptr_t>(base) & 15u;
-  if (r == 0) return load_stream(base + off);
-  const uint8_t* b = base - r + off;
-  const uint4 lo = load_stream(b), hi = load_stream(b + 16);
-  const uint32_t sh = r & 3u;
-  switch (r >> 2) {
-    case 0: return align_words<0>(lo, hi, sh);
-    case 1: return align_words<1>(lo, hi, sh);
-    case 2: return align_words<2>(lo, hi, sh);
-    default: return align_words<3>(lo, hi, sh);
-  }
+  if ((reinterpret_cast<uintptr_t>(base) & 15u) == 0) return load_stream(base + off);
+  const u32x4_unaligned v =
+      __builtin_nontemporal_load(reinterpret_cast<const u32x4_unaligned*>(base + off));
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // ---------------------------------------------------------- unit access --
