@@ -314,9 +314,11 @@ constexpr int kWidePair() {
 // 16 bytes at base + off, where off is a multiple of 16 and base may have any
 // alignment r = base mod 16 (uniform: it depends on the shard only).  r = 0
 // is the aligned dwordx4 load; otherwise one dwordx4 load at the unaligned
-// address (the vector type below has alignment 1, so the compiler neither
-// splits the load nor assumes its alignment; the hardware takes unaligned
-// addresses), non-temporal like the aligned one.  It reads exactly the 16
+// address (the vector type below has alignment 1, so the compiler does not
+// assume an alignment; for gfx950 it emits the single dwordx4 all the same,
+// as it does for any 16-byte memcpy from a byte pointer, since the ROCm
+// driver runs compute queues with unaligned memory access enabled),
+// non-temporal like the aligned one.  It reads exactly the 16
 // bytes asked for.  Measured on MI355X against the former form (the two
 // aligned blocks holding the bytes, shifted into place with
 // v_alignbyte_b32), HBM traffic, TB/s, one box: 600 fp32 tensor views of one
